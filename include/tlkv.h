@@ -1,0 +1,151 @@
+/*
+ * tlkv.h — C ABI of the MI355X (gfx950) KV-cache device library.
+ *
+ * Plain C: pointers, sizes and a stream handle.  All pointers named "device"
+ * are HIP device addresses; `stream` is a hipStream_t passed as void* (NULL =
+ * the default stream).  Every entry point returns 0 on success or a negative
+ * TL_E* code; tl_last_error() gives the message of the calling thread's last
+ * failure.  No entry point aborts the process (the reference's CUDA backend
+ * exits on API errors, src/backend/gpu/gpu.h:41-50; here they are returned,
+ * the same way kvcache.c returns false).
+ *
+ * Reference interfaces replaced (paths relative to the tinyllama.c tree):
+ *   tl_kv_append      the K/V write-through of OP_ATTN:
+ *                     src/backend/cpu/cpu_op.c:995-1008 (slot-indexed) and
+ *                     src/backend/gpu/gpu_op.cu:632-644,947-951 (k_kv_write)
+ *   tl_attn           OP_ATTN as a whole: cpu_op.c:964-1064 (op_attn) and
+ *                     gpu_op.cu:925-962 (gpu_op_attn) — append, then causal
+ *                     GQA attention over the slot table with the optional
+ *                     sliding window (cpu_op.c:1019-1022)
+ *   tl_attn_decode_batch  one-token OP_ATTN for several sessions in one
+ *                     launch (the -np slots of src/server.c:1464-1478 are
+ *                     independent Sessions, each with its own KvCache)
+ *   tl_kv_gather      read view of the cache rows (the rows op_attn reads at
+ *                     cpu_op.c:1024-1033,1045-1052)
+ *   tl_kv_copy        slot-row copy across all layers: prefix fork and
+ *                     eviction compaction (no counterpart: the reference shares
+ *                     slots in place, src/kvcache.c:192-218)
+ *   tl_rope           OP_ROPE_NORM / OP_ROPE_NEOX, cpu_op.c:632-700,
+ *                     gpu_op.cu:300-355
+ *
+ * Cache layout (per layer, per K and V): f16 bits [n_kv_head][cap][head_dim],
+ * the reference's head-major layout (src/graph.c:852-858, AttnKvCache in
+ * src/def.h:289-294) with binary16 elements instead of f32.  The f16 value of
+ * a row element is the IEEE round-to-nearest-even of the f32 input; NaN maps
+ * to a quiet NaN that keeps the sign and the top 9 payload bits.
+ */
+#ifndef TLKV_H
+#define TLKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TL_OK        = 0,
+    TL_EINVAL    = -1,   /* bad argument / shape the kernels do not support */
+    TL_ERANGE    = -2,   /* slot or position outside the cache */
+    TL_EHIP      = -3,   /* HIP runtime error */
+    TL_ENOMEM    = -4,   /* device allocation failed */
+};
+
+/* One layer of the KV cache (the device twin of AttnKvCache). */
+typedef struct tl_kv_layer {
+    void     *k;          /* device, f16 [n_kv_head][cap][head_dim] */
+    void     *v;          /* device, f16 [n_kv_head][cap][head_dim] */
+    uint32_t  cap;        /* rows per head */
+    uint32_t  n_kv_head;
+    uint32_t  head_dim;   /* kv_head_dim: 64, 128 or 256 */
+    uint32_t  ring;       /* 0: rows addressed through the slot table;
+                             R > 0: physical row of position p is p % R
+                             (sliding-window layers; R <= cap) */
+} tl_kv_layer;
+
+/* Arguments of one OP_ATTN call (the fields of OpCtx, src/def.h:550-565,
+ * that op_attn reads). */
+typedef struct tl_attn_args {
+    const float    *q;        /* device [n][q_stride] f32, RoPE'd */
+    const float    *k;        /* device [n][kv_stride] f32, RoPE'd new rows */
+    const float    *v;        /* device [n][kv_stride] f32 new rows */
+    float          *dst;      /* device [n][q_stride] f32 */
+    const uint32_t *slots;    /* device slot table, logical pos -> row, at
+                                 least pos+n entries; NULL = identity */
+    uint32_t        pos;      /* absolute position of batch row 0 */
+    uint32_t        n;        /* batch rows */
+    uint32_t        n_head;   /* q heads (multiple of n_kv_head, ratio <= 8) */
+    uint32_t        q_stride; /* floats between q / dst rows (>= n_head*head_dim) */
+    uint32_t        kv_stride;/* floats between k / v rows (>= n_kv*head_dim) */
+    uint32_t        window;   /* sliding window, 0 = full causal */
+    float           scale;    /* 1/sqrt(kv_head_dim) in the reference (graph.c:1275) */
+} tl_attn_args;
+
+/* One session of a batched one-token decode. */
+typedef struct tl_decode_seq {
+    tl_kv_layer     layer;
+    const uint32_t *slots;    /* device slot table of this session, or NULL */
+    uint32_t        pos;      /* position of the new token */
+    uint32_t        pad_;
+    const float    *q;        /* device [n_head*head_dim] f32 */
+    const float    *k;        /* device [n_kv*head_dim] f32 */
+    const float    *v;        /* device [n_kv*head_dim] f32 */
+    float          *dst;      /* device [n_head*head_dim] f32 */
+} tl_decode_seq;
+
+#define TL_MAX_BATCH_SEQ 16
+
+const char *tl_last_error(void);
+
+/* Select the device for the calling thread and set up library state. */
+int tl_init(int device);
+
+/* Allocate / free one layer's K and V storage (hipMalloc, contents zero). */
+int tl_kv_layer_alloc(tl_kv_layer *L, uint32_t cap, uint32_t n_kv_head,
+                      uint32_t head_dim, uint32_t ring);
+int tl_kv_layer_free(tl_kv_layer *L);
+
+/* Write n rows of K and V (f32 -> f16 RNE) at slots[pos+i] (or pos+i when
+ * slots is NULL, or (pos+i) % ring on ring layers).  Rows whose slot is
+ * outside the cache are skipped on the device; callers validate slots on the
+ * host (the session layer does). */
+int tl_kv_append(const tl_kv_layer *L, const float *k, const float *v,
+                 uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                 uint32_t n, void *stream);
+
+/* Copy rows slots[i] of every head to k_out/v_out [n][n_kv_head][head_dim]
+ * f16 (device).  slots: device [n]. */
+int tl_kv_gather(const tl_kv_layer *L, const uint32_t *slots, uint32_t n,
+                 uint16_t *k_out, uint16_t *v_out, void *stream);
+
+/* For every layer in layers[0..n_layer) (host array) copy row src[i] to row
+ * dst[i] in K and V, all heads.  src/dst: device [n].  The destination rows
+ * must not be source rows of the same call. */
+int tl_kv_copy(const tl_kv_layer *layers, uint32_t n_layer,
+               const uint32_t *src, const uint32_t *dst, uint32_t n,
+               void *stream);
+
+/* OP_ATTN: append the batch rows, then attend.  Decode-sized batches use the
+ * split-K LDS kernel, larger ones the MFMA chunked-prefill kernel. */
+int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
+
+/* Attention only (no append): the rows at positions < pos+n are assumed
+ * already in the cache. */
+int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
+
+/* One-token OP_ATTN (append + attention) for n_seq sessions in one launch.
+ * All sessions share n_kv_head, head_dim and n_head. */
+int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
+                         uint32_t n_head, uint32_t window, float scale,
+                         void *stream);
+
+/* OP_ROPE_NORM (neox = 0) / OP_ROPE_NEOX (neox = 1) in place on x
+ * [rows][row_stride] f32, row p at position pos+p. */
+int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t heads,
+            uint32_t head_dim, uint32_t rope_dim, uint32_t pos, float theta,
+            int neox, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,323 @@
+"""GPU parity of the device path against the CPU oracle (through the C ABI).
+
+Append / gather / copy: bit-exact against oracle.c (f16 RNE of the reference's
+f32 rows, written at the reference's slot, cpu_op.c:995-1008).
+Attention: within 2e-3 max-abs of the oracle's op_attn restatement, both over
+the same f16 cache (kernel error alone) and over the reference's f32 cache
+(the reference CPU semantics).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def T():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import tlkv
+    tlkv.check(tlkv.lib().tl_init(0))
+    return torch
+
+
+_KEEP = []
+
+
+def dev(T, a):
+    """Device copy of a numpy array.  The tensor is kept alive until the
+    module ends: kernels run asynchronously and only its address crosses the
+    ABI, so a temporary could be freed and reused before the kernel reads it."""
+    t = T.from_numpy(np.ascontiguousarray(a)).cuda()
+    _KEEP.append(t)
+    return t
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def sync(T):
+    T.cuda.synchronize()
+    _KEEP.clear()
+
+
+def rows(rng, n, width, special=False):
+    x = rng.standard_normal((n, width)).astype(np.float32)
+    if special:
+        sp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65520.0, 1e-8,
+                       -6.0e-8, 2.9802322e-08, 5.9604645e-08, 1e5, -3e-5, 0.5 + 2**-12],
+                      dtype=np.float32)
+        flat = x.reshape(-1)
+        flat[:sp.size] = sp
+        # a signalling-pattern NaN with payload
+        flat[sp.size] = np.frombuffer(np.uint32(0x7f800123).tobytes(), np.float32)[0]
+        flat[sp.size + 1] = np.frombuffer(np.uint32(0xffc00001).tobytes(), np.float32)[0]
+    return x
+
+
+@pytest.mark.parametrize("n_kv,hd,cap,n,pos,perm", [
+    (8, 128, 64, 17, 5, True),
+    (8, 64, 40, 33, 0, False),
+    (4, 256, 32, 9, 3, True),
+    (4, 128, 600, 512, 7, True),
+])
+def test_append_bitexact(T, n_kv, hd, cap, n, pos, perm):
+    import tlkv
+    rng = np.random.default_rng(n * 31 + hd)
+    k = rows(rng, n, n_kv * hd, special=True)
+    v = rows(rng, n, n_kv * hd, special=True)
+    slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    L = tlkv.Layer(cap, n_kv, hd)
+    ds = dev(T, slots)
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, k)), tlkv.ptr(dev(T, v)),
+                                       n_kv * hd, tlkv.ptr(ds), pos, n, None))
+    sync(T)
+    C = O.Cache(cap, n_kv, hd)
+    assert C.append(k, v, slots, pos, n) == 0
+    assert np.array_equal(host(L.k).view(np.uint16), C.k)
+    assert np.array_equal(host(L.v).view(np.uint16), C.v)
+
+
+def test_append_identity_slots(T):
+    import tlkv
+    rng = np.random.default_rng(3)
+    n_kv, hd, cap = 8, 128, 48
+    k, v = rows(rng, 20, n_kv * hd), rows(rng, 20, n_kv * hd)
+    L = tlkv.Layer(cap, n_kv, hd)
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, k)), tlkv.ptr(dev(T, v)),
+                                       n_kv * hd, None, 11, 20, None))
+    sync(T)
+    C = O.Cache(cap, n_kv, hd)
+    C.append(k, v, None, 11, 20)
+    assert np.array_equal(host(L.k).view(np.uint16), C.k)
+    assert np.array_equal(host(L.v).view(np.uint16), C.v)
+
+
+def test_gather_roundtrip(T):
+    """gather(append(x)) == f16(x) for any slot permutation."""
+    import tlkv
+    rng = np.random.default_rng(4)
+    n_kv, hd, cap, n = 4, 128, 256, 200
+    k, v = rows(rng, n, n_kv * hd, True), rows(rng, n, n_kv * hd, True)
+    slots = rng.permutation(cap).astype(np.uint32)
+    L = tlkv.Layer(cap, n_kv, hd)
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, k)), tlkv.ptr(dev(T, v)),
+                                       n_kv * hd, tlkv.ptr(dev(T, slots)), 0, n, None))
+    ko = T.zeros((n, n_kv, hd), dtype=T.float16, device="cuda")
+    vo = T.zeros_like(ko)
+    tlkv.check(tlkv.lib().tl_kv_gather(L.desc, tlkv.ptr(dev(T, slots[:n])), n,
+                                       tlkv.ptr(ko), tlkv.ptr(vo), None))
+    sync(T)
+    assert np.array_equal(host(ko).view(np.uint16).reshape(n, -1), O.f16_bits(k))
+    assert np.array_equal(host(vo).view(np.uint16).reshape(n, -1), O.f16_bits(v))
+
+
+def test_copy_rows_all_layers(T):
+    import tlkv
+    rng = np.random.default_rng(5)
+    n_kv, hd, cap, nl = 4, 128, 64, 3
+    layers = [tlkv.Layer(cap, n_kv, hd) for _ in range(nl)]
+    for L in layers:
+        L.k.copy_(T.randn(L.k.shape, device="cuda").half())
+        L.v.copy_(T.randn(L.v.shape, device="cuda").half())
+    before = [(host(L.k).copy(), host(L.v).copy()) for L in layers]
+    src = np.array([1, 5, 9, 30, 31], dtype=np.uint32)
+    dst = np.array([40, 2, 63, 0, 10], dtype=np.uint32)
+    arr = (tlkv.KvLayer * nl)(*[L.desc for L in layers])
+    tlkv.check(tlkv.lib().tl_kv_copy(arr, nl, tlkv.ptr(dev(T, src)),
+                                     tlkv.ptr(dev(T, dst)), src.size, None))
+    sync(T)
+    for L, (kb, vb) in zip(layers, before):
+        ke, ve = kb.copy(), vb.copy()
+        ke[:, dst] = kb[:, src]
+        ve[:, dst] = vb[:, src]
+        assert np.array_equal(host(L.k), ke)
+        assert np.array_equal(host(L.v), ve)
+
+
+def _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots, seed, ring=0):
+    """Fill positions [0,pos) then run OP_ATTN on rows [pos,pos+n) on both the
+    device and the oracle.  Returns (device, oracle f16 cache, oracle f32 cache)."""
+    import tlkv
+    rng = np.random.default_rng(seed)
+    kd = n_kv * hd
+    hist_k, hist_v = rows(rng, pos, kd), rows(rng, pos, kd)
+    q = rows(rng, n, n_head * hd)
+    k, v = rows(rng, n, kd), rows(rng, n, kd)
+
+    L = tlkv.Layer(cap, n_kv, hd, ring=ring)
+    ds = None if slots is None else dev(T, slots)
+    Cf16 = O.Cache(cap, n_kv, hd, f16=True)
+    Cf32 = O.Cache(cap, n_kv, hd, f16=False)
+    if pos:
+        if ring:
+            for p in range(pos):
+                tlkv.check(tlkv.lib().tl_kv_append(
+                    L.desc, tlkv.ptr(dev(T, hist_k[p:p + 1])),
+                    tlkv.ptr(dev(T, hist_v[p:p + 1])), kd, None, p, 1, None))
+                Cf16.append(hist_k[p:p + 1], hist_v[p:p + 1], None, p % ring, 1)
+                Cf32.append(hist_k[p:p + 1], hist_v[p:p + 1], None, p % ring, 1)
+        else:
+            tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, hist_k)),
+                                               tlkv.ptr(dev(T, hist_v)), kd, tlkv.ptr(ds),
+                                               0, pos, None))
+            Cf16.append(hist_k, hist_v, slots, 0, pos)
+            Cf32.append(hist_k, hist_v, slots, 0, pos)
+    dq, dk, dv = dev(T, q), dev(T, k), dev(T, v)
+    out = T.zeros((n, n_head * hd), dtype=T.float32, device="cuda")
+    a = tlkv.attn_args(dq, dk, dv, out, ds, pos, n, n_head, hd, n_kv, window,
+                       O.scale_of(hd))
+    tlkv.check(tlkv.lib().tl_attn(L.desc, a, None))
+    sync(T)
+    o16 = O.attn(Cf16, q, k, v, slots, pos, n, n_head, window=window, ring=ring)
+    o32 = O.attn(Cf32, q, k, v, slots, pos, n, n_head, window=window, ring=ring)
+    return host(out), o16, o32, L, Cf16
+
+
+ATTN_CASES = [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted slots
+    (32, 8, 64, 1024, 700, 1, 0, True),      # config 1 shape
+    (28, 4, 128, 2048, 1500, 1, 0, True),    # config 2/3 shape, gqa 7
+    (32, 8, 128, 4096, 4000, 1, 0, False),   # config 4 shape
+    (8, 4, 256, 2048, 1800, 1, 1024, True),  # config 5 local layer
+    (8, 4, 256, 2048, 1800, 1, 0, False),    # config 5 global layer
+    (32, 8, 128, 512, 3, 1, 0, True),        # tiny history
+    (32, 8, 128, 512, 0, 1, 0, False),       # first token
+    (16, 2, 128, 600, 200, 5, 0, True),      # multi-row batch (decode kernel)
+    (16, 2, 128, 600, 200, 6, 64, True),     # multi-row + window
+    (8, 8, 64, 300, 100, 3, 0, False),       # MHA
+]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attn_vs_oracle(T, case):
+    n_head, n_kv, hd, cap, pos, n, window, perm = case
+    rng = np.random.default_rng(hash(case) & 0xffff)
+    slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                    seed=pos + n)
+    e16 = np.abs(out - o16).max()
+    e32 = np.abs(out - o32).max()
+    assert e16 < TOL, f"vs f16-cache oracle {e16}"
+    assert e32 < TOL, f"vs f32-cache (reference) oracle {e32}"
+
+
+def test_attn_noncontiguous_equals_contiguous(T):
+    """Spec'd parity test of the reference design (slot table [7,3,9,12] vs
+    [0,1,2,3]): identical outputs."""
+    n_head, n_kv, hd = 8, 2, 64
+    cap = 16
+    perm = np.arange(cap, dtype=np.uint32)
+    perm[:4] = [7, 3, 9, 12]
+    perm[4:] = [s for s in range(cap) if s not in (7, 3, 9, 12)]
+    ident = np.arange(cap, dtype=np.uint32)
+    a, _, _, _, _ = _run_attn(T, n_head, n_kv, hd, cap, 3, 1, 0, perm, seed=9)
+    b, _, _, _, _ = _run_attn(T, n_head, n_kv, hd, cap, 3, 1, 0, ident, seed=9)
+    assert np.array_equal(a, b)
+
+
+def test_attn_ring_window(T):
+    """Ring layout for windowed layers equals the masked full cache."""
+    n_head, n_kv, hd, win = 8, 4, 256, 64
+    ring = win
+    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, 256, 200, 1, win, None,
+                                    seed=11, ring=ring)
+    assert np.abs(out - o32).max() < TOL
+    assert np.abs(out - o16).max() < TOL
+
+
+def test_attn_closed_form_identical_keys(T):
+    """All keys equal -> uniform softmax -> output = mean of V rows (f16)."""
+    import tlkv
+    n_head, n_kv, hd, P = 8, 2, 128, 3000
+    cap = P
+    rng = np.random.default_rng(12)
+    L = tlkv.Layer(cap, n_kv, hd)
+    krow = rng.standard_normal(n_kv * hd).astype(np.float32)
+    hk = np.tile(krow, (P - 1, 1))
+    hv = rows(rng, P - 1, n_kv * hd)
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, hk)), tlkv.ptr(dev(T, hv)),
+                                       n_kv * hd, None, 0, P - 1, None))
+    q = rows(rng, 1, n_head * hd)
+    v_new = rows(rng, 1, n_kv * hd)
+    out = T.zeros((1, n_head * hd), dtype=T.float32, device="cuda")
+    a = tlkv.attn_args(dev(T, q), dev(T, krow[None]), dev(T, v_new), out, None,
+                       P - 1, 1, n_head, hd, n_kv, 0, O.scale_of(hd))
+    tlkv.check(tlkv.lib().tl_attn(L.desc, a, None))
+    sync(T)
+    allv = O.f16_to_f32(O.f16_bits(np.concatenate([hv, v_new]))).astype(np.float64)
+    mean = allv.mean(axis=0).reshape(n_kv, hd)
+    expect = np.repeat(mean, n_head // n_kv, axis=0).reshape(-1)
+    assert np.abs(host(out)[0] - expect).max() < 1e-4
+
+
+def test_split_count_invariance(T):
+    """The split-K decomposition does not change the result beyond rounding."""
+    outs = []
+    for wgs in ("1", "64", "4096"):
+        os.environ["TL_DECODE_WGS"] = wgs
+        try:
+            out, o16, _, _, _ = _run_attn(T, 32, 8, 128, 8192, 8000, 1, 0, None, seed=13)
+        finally:
+            del os.environ["TL_DECODE_WGS"]
+        assert np.abs(out - o16).max() < TOL
+        outs.append(out)
+    assert np.abs(outs[0] - outs[1]).max() < 1e-5
+    assert np.abs(outs[0] - outs[2]).max() < 1e-5
+
+
+def test_decode_batch_sessions(T):
+    """Multi-session one-token decode equals per-session OP_ATTN."""
+    import tlkv
+    n_head, n_kv, hd = 28, 4, 128
+    n_seq = 8
+    rng = np.random.default_rng(14)
+    seqs, refs, keep = [], [], []
+    for s in range(n_seq):
+        cap = 512 + 64 * s
+        pos = 300 + 17 * s
+        slots = rng.permutation(cap).astype(np.uint32)
+        L = tlkv.Layer(cap, n_kv, hd)
+        hk, hv = rows(rng, pos, n_kv * hd), rows(rng, pos, n_kv * hd)
+        ds = dev(T, slots)
+        tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, hk)),
+                                           tlkv.ptr(dev(T, hv)), n_kv * hd,
+                                           tlkv.ptr(ds), 0, pos, None))
+        C = O.Cache(cap, n_kv, hd)
+        C.append(hk, hv, slots, 0, pos)
+        q, k, v = rows(rng, 1, n_head * hd), rows(rng, 1, n_kv * hd), rows(rng, 1, n_kv * hd)
+        dq, dk, dv = dev(T, q), dev(T, k), dev(T, v)
+        out = T.zeros((1, n_head * hd), dtype=T.float32, device="cuda")
+        keep += [L, ds, dq, dk, dv]
+        seqs.append(tlkv.DecodeSeq(L.desc, ds.data_ptr(), pos, 0, dq.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), out.data_ptr()))
+        refs.append((out, O.attn(C, q, k, v, slots, pos, 1, n_head)))
+    arr = (tlkv.DecodeSeq * n_seq)(*seqs)
+    tlkv.check(tlkv.lib().tl_attn_decode_batch(arr, n_seq, n_head, 0,
+                                               O.scale_of(hd), None))
+    sync(T)
+    for out, ref in refs:
+        assert np.abs(host(out) - ref).max() < TOL
+
+
+@pytest.mark.parametrize("neox", [0, 1])
+def test_rope_vs_oracle(T, neox):
+    import tlkv
+    rng = np.random.default_rng(15 + neox)
+    heads, hd, rows_n, pos = 8, 128, 64, 3000
+    x = rng.standard_normal((rows_n, heads * hd)).astype(np.float32)
+    dx = dev(T, x)
+    tlkv.check(tlkv.lib().tl_rope(tlkv.ptr(dx), rows_n, heads * hd, heads, hd, hd, pos,
+                                  500000.0, neox, None))
+    sync(T)
+    ref = O.rope(x, heads, hd, hd, pos, 500000.0, neox)
+    # angles up to ~3e3 rad: one f32 ulp of the angle is ~2.4e-4 rad; libm
+    # (reference: -ffast-math glibc) and the device differ by a few ulp
+    assert np.abs(host(dx) - ref).max() < 2e-3

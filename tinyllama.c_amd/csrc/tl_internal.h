@@ -1,0 +1,61 @@
+/* tl_internal.h — launch parameter blocks shared by the .hip translation units. */
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/tlkv.h"
+
+#define TL_COPY_MAX_LAYERS 64
+#define TL_PREFILL_MIN_ROWS 16
+
+/* One segment of an append launch: n rows of one layer of one session. */
+struct AppendSeg {
+    uint16_t *kc, *vc;
+    const float *k, *v;
+    const uint32_t *slots;
+    uint32_t cap, ring, n_kv, head_dim, kv_stride, pos, n;
+};
+struct AppendParams {
+    AppendSeg seg[TL_MAX_BATCH_SEQ];
+};
+
+struct CopyParams {
+    uint16_t *k[TL_COPY_MAX_LAYERS];
+    uint16_t *v[TL_COPY_MAX_LAYERS];
+    uint32_t cap, n_kv, head_dim;
+};
+
+/* One sequence of a decode launch (rows_per_seq rows at positions pos..). */
+struct DecSeq {
+    const uint16_t *k, *v;
+    const uint32_t *slots;
+    const float *q;
+    float *dst;
+    uint32_t cap, ring, pos;
+};
+struct DecParams {
+    DecSeq seq[TL_MAX_BATCH_SEQ];
+    uint32_t rows_per_seq;
+    uint32_t n_kv, n_head, q_stride, window;
+    float scale_log2;
+    uint32_t chunk, n_split;
+    float *ws_acc;
+    float2 *ws_ml;
+    uint32_t *counters;
+};
+
+struct TlWorkspace {
+    float *acc;
+    float *ml;
+    uint32_t *cnt;
+    size_t acc_cap, ml_cap, cnt_cap;
+};
+
+int tl_fail(int code, const char *fmt, ...);
+int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters, TlWorkspace **out);
+int tl_launch_append(const AppendParams &p, uint32_t n_seg, hipStream_t stream);
+int tl_launch_decode(DecParams &p, uint32_t n_rows_total, uint32_t head_dim, uint32_t G,
+                     uint32_t max_vis, hipStream_t st);
+
+/* MFMA chunked-prefill attention (tl_prefill.hip). */
+bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a);
+int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st);

@@ -1,0 +1,787 @@
+/*
+ * tl_kv.hip — gfx950 kernels and C ABI for the KV-cache hot path.
+ *
+ *   kv_append_kernel    OP_ATTN's K/V write-through (reference:
+ *                       src/backend/cpu/cpu_op.c:995-1008), f32 -> f16 RNE,
+ *                       one 16-byte store per 8 elements.
+ *   kv_gather_kernel    read rows by slot.
+ *   kv_copy_kernel      row copies across all layers (fork / compaction).
+ *   rope_kernel         OP_ROPE_NORM / OP_ROPE_NEOX (cpu_op.c:632-700).
+ *   attn_decode_kernel  split-K ("flash-decoding") attention over the slot
+ *                       table, one workgroup per (split, kv-head, row) serving
+ *                       all q-heads of the GQA group; scores and softmax in
+ *                       f32 with per-lane-group online softmax, wave merges
+ *                       through DPP/shuffles, workgroup merge through LDS and
+ *                       a last-workgroup LSE merge of the splits.
+ *                       Math of cpu_op.c:1011-1062.
+ * The MFMA chunked-prefill kernel lives in tl_prefill.hip.
+ */
+#include "tl_common.h"
+#include "tl_internal.h"
+#include "../../include/tlkv.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* errors                                                                    */
+/* ------------------------------------------------------------------------ */
+
+static thread_local char g_err[512] = "";
+
+int tl_fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+extern "C" const char *tl_last_error(void) { return g_err; }
+
+#define HIP_TRY(expr)                                                         \
+    do {                                                                      \
+        hipError_t e_ = (expr);                                               \
+        if (e_ != hipSuccess)                                                 \
+            return tl_fail(TL_EHIP, "%s: %s", #expr, hipGetErrorString(e_));  \
+    } while (0)
+
+/* ------------------------------------------------------------------------ */
+/* per-device workspace for split-K partials                                 */
+/* ------------------------------------------------------------------------ */
+
+#define TL_MAX_DEV 16
+static TlWorkspace g_ws[TL_MAX_DEV];
+
+int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters,
+                     TlWorkspace **out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", dev);
+    TlWorkspace *w = &g_ws[dev];
+    if (acc_floats > w->acc_cap) {
+        if (w->acc) HIP_TRY(hipFree(w->acc));
+        w->acc = NULL;
+        size_t cap = acc_floats + acc_floats / 4 + 1024;
+        if (hipMalloc((void **)&w->acc, cap * sizeof(float)) != hipSuccess)
+            return tl_fail(TL_ENOMEM, "workspace: %zu floats", cap);
+        w->acc_cap = cap;
+    }
+    if (ml_pairs > w->ml_cap) {
+        if (w->ml) HIP_TRY(hipFree(w->ml));
+        w->ml = NULL;
+        size_t cap = ml_pairs + ml_pairs / 4 + 256;
+        if (hipMalloc((void **)&w->ml, cap * sizeof(float2)) != hipSuccess)
+            return tl_fail(TL_ENOMEM, "workspace: %zu pairs", cap);
+        w->ml_cap = cap;
+    }
+    if (counters > w->cnt_cap) {
+        if (w->cnt) HIP_TRY(hipFree(w->cnt));
+        w->cnt = NULL;
+        size_t cap = counters + 256;
+        if (hipMalloc((void **)&w->cnt, cap * sizeof(u32)) != hipSuccess)
+            return tl_fail(TL_ENOMEM, "workspace: %zu counters", cap);
+        /* Counters start at zero once; every launch leaves them at zero. */
+        HIP_TRY(hipMemset(w->cnt, 0, cap * sizeof(u32)));
+        HIP_TRY(hipDeviceSynchronize());
+        w->cnt_cap = cap;
+    }
+    *out = w;
+    return TL_OK;
+}
+
+extern "C" int tl_init(int device) {
+    HIP_TRY(hipSetDevice(device));
+    TlWorkspace *w;
+    return tl_workspace_get(1 << 20, 1 << 14, 4096, &w);
+}
+
+/* ------------------------------------------------------------------------ */
+/* layer storage                                                             */
+/* ------------------------------------------------------------------------ */
+
+static int check_layer(const tl_kv_layer *L) {
+    if (!L || !L->k || !L->v) return tl_fail(TL_EINVAL, "layer: null storage");
+    if (L->head_dim != 64 && L->head_dim != 128 && L->head_dim != 256)
+        return tl_fail(TL_EINVAL, "head_dim %u unsupported (64/128/256)", L->head_dim);
+    if (L->n_kv_head == 0 || L->cap == 0)
+        return tl_fail(TL_EINVAL, "layer: empty shape");
+    if (L->ring > L->cap) return tl_fail(TL_EINVAL, "ring %u > cap %u", L->ring, L->cap);
+    if (((uintptr_t)L->k | (uintptr_t)L->v) & 15)
+        return tl_fail(TL_EINVAL, "cache storage not 16-byte aligned");
+    return TL_OK;
+}
+
+extern "C" int tl_kv_layer_alloc(tl_kv_layer *L, uint32_t cap, uint32_t n_kv_head,
+                                 uint32_t head_dim, uint32_t ring) {
+    if (!L) return tl_fail(TL_EINVAL, "null layer");
+    memset(L, 0, sizeof(*L));
+    size_t bytes = (size_t)cap * n_kv_head * head_dim * sizeof(u16);
+    if (bytes == 0) return tl_fail(TL_EINVAL, "empty layer");
+    if (hipMalloc(&L->k, bytes) != hipSuccess) {
+        L->k = NULL;
+        return tl_fail(TL_ENOMEM, "layer K: %zu bytes", bytes);
+    }
+    if (hipMalloc(&L->v, bytes) != hipSuccess) {
+        (void)hipFree(L->k);
+        L->k = NULL;
+        L->v = NULL;
+        return tl_fail(TL_ENOMEM, "layer V: %zu bytes", bytes);
+    }
+    HIP_TRY(hipMemset(L->k, 0, bytes));
+    HIP_TRY(hipMemset(L->v, 0, bytes));
+    L->cap = cap;
+    L->n_kv_head = n_kv_head;
+    L->head_dim = head_dim;
+    L->ring = ring;
+    return check_layer(L);
+}
+
+extern "C" int tl_kv_layer_free(tl_kv_layer *L) {
+    if (!L) return TL_OK;
+    if (L->k) HIP_TRY(hipFree(L->k));
+    if (L->v) HIP_TRY(hipFree(L->v));
+    L->k = L->v = NULL;
+    return TL_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* append / gather / copy                                                    */
+/* ------------------------------------------------------------------------ */
+
+TL_DEV u32 phys_row(u32 p, u32 ring, const u32 *slots) {
+    return ring ? p % ring : (slots ? slots[p] : p);
+}
+
+TL_DEV uint4 cvt8(const float *src) {
+    float4 a = *(const float4 *)src;
+    float4 b = *(const float4 *)(src + 4);
+    uint4 o;
+    o.x = pack_f16x2(a.x, a.y);
+    o.y = pack_f16x2(a.z, a.w);
+    o.z = pack_f16x2(b.x, b.y);
+    o.w = pack_f16x2(b.z, b.w);
+    return o;
+}
+
+/* grid: (blocks, n_seg).  One thread per 8-element vector of one row of one
+ * head; consecutive threads cover consecutive 16-byte pieces of a row. */
+__global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
+    const AppendSeg &sg = p.seg[blockIdx.y];
+    const u32 vpr = sg.head_dim >> 3;
+    const u64 total = (u64)sg.n * sg.n_kv * vpr;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        u32 c = (u32)(idx % vpr);
+        u64 t = idx / vpr;
+        u32 h = (u32)(t % sg.n_kv);
+        u32 i = (u32)(t / sg.n_kv);
+        u32 slot = phys_row(sg.pos + i, sg.ring, sg.slots);
+        if (slot >= sg.cap) continue;
+        u64 src = (u64)i * sg.kv_stride + (u64)h * sg.head_dim + c * 8;
+        u64 dst = ((u64)h * sg.cap + slot) * sg.head_dim + c * 8;
+        *(uint4 *)(sg.kc + dst) = cvt8(sg.k + src);
+        *(uint4 *)(sg.vc + dst) = cvt8(sg.v + src);
+    }
+}
+
+int tl_launch_append(const AppendParams &p, u32 n_seg, hipStream_t stream) {
+    u64 most = 0;
+    for (u32 s = 0; s < n_seg; s++) {
+        u64 t = (u64)p.seg[s].n * p.seg[s].n_kv * (p.seg[s].head_dim >> 3);
+        if (t > most) most = t;
+    }
+    if (most == 0) return TL_OK;
+    u64 blocks = (most + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(kv_append_kernel, dim3((u32)blocks, n_seg), dim3(256), 0,
+                       stream, p);
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+static int fill_seg(AppendSeg &sg, const tl_kv_layer *L, const float *k,
+                    const float *v, u32 kv_stride, const u32 *slots, u32 pos,
+                    u32 n) {
+    if (!k || !v) return tl_fail(TL_EINVAL, "append: null rows");
+    if (kv_stride < L->n_kv_head * L->head_dim || (kv_stride & 3) ||
+        (((uintptr_t)k | (uintptr_t)v) & 15))
+        return tl_fail(TL_EINVAL, "append: rows must be 16-byte aligned, stride %u", kv_stride);
+    sg.kc = (u16 *)L->k;
+    sg.vc = (u16 *)L->v;
+    sg.k = k;
+    sg.v = v;
+    sg.slots = slots;
+    sg.cap = L->cap;
+    sg.ring = L->ring;
+    sg.n_kv = L->n_kv_head;
+    sg.head_dim = L->head_dim;
+    sg.kv_stride = kv_stride;
+    sg.pos = pos;
+    sg.n = n;
+    return TL_OK;
+}
+
+extern "C" int tl_kv_append(const tl_kv_layer *L, const float *k, const float *v,
+                            uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                            uint32_t n, void *stream) {
+    int rc = check_layer(L);
+    if (rc) return rc;
+    if (n == 0) return TL_OK;
+    AppendParams p;
+    memset(&p, 0, sizeof(p));
+    rc = fill_seg(p.seg[0], L, k, v, kv_stride, slots, pos, n);
+    if (rc) return rc;
+    return tl_launch_append(p, 1, (hipStream_t)stream);
+}
+
+__global__ __launch_bounds__(256) void kv_gather_kernel(
+    const u16 *kc, const u16 *vc, u32 cap, u32 n_kv, u32 head_dim,
+    const u32 *slots, u32 n, u16 *ko, u16 *vo) {
+    const u32 vpr = head_dim >> 3;
+    const u64 total = (u64)n * n_kv * vpr;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        u32 c = (u32)(idx % vpr);
+        u64 t = idx / vpr;
+        u32 h = (u32)(t % n_kv);
+        u32 i = (u32)(t / n_kv);
+        u32 slot = slots[i];
+        uint4 kk = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+        if (slot < cap) {
+            u64 src = ((u64)h * cap + slot) * head_dim + c * 8;
+            kk = *(const uint4 *)(kc + src);
+            vv = *(const uint4 *)(vc + src);
+        }
+        u64 dst = ((u64)i * n_kv + h) * head_dim + c * 8;
+        *(uint4 *)(ko + dst) = kk;
+        *(uint4 *)(vo + dst) = vv;
+    }
+}
+
+extern "C" int tl_kv_gather(const tl_kv_layer *L, const uint32_t *slots, uint32_t n,
+                            uint16_t *k_out, uint16_t *v_out, void *stream) {
+    int rc = check_layer(L);
+    if (rc) return rc;
+    if (n == 0) return TL_OK;
+    if (!slots || !k_out || !v_out) return tl_fail(TL_EINVAL, "gather: null pointer");
+    if (((uintptr_t)k_out | (uintptr_t)v_out) & 15)
+        return tl_fail(TL_EINVAL, "gather: outputs not 16-byte aligned");
+    u64 total = (u64)n * L->n_kv_head * (L->head_dim >> 3);
+    u64 blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(kv_gather_kernel, dim3((u32)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const u16 *)L->k, (const u16 *)L->v,
+                       L->cap, L->n_kv_head, L->head_dim, slots, n, k_out, v_out);
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+/* grid: (blocks, layers-in-batch).  Copies one 16-byte vector per thread. */
+__global__ __launch_bounds__(256) void kv_copy_kernel(const CopyParams p,
+                                                      const u32 *src, const u32 *dst,
+                                                      u32 n) {
+    const u32 l = blockIdx.y;
+    u16 *kc = p.k[l];
+    u16 *vc = p.v[l];
+    const u32 vpr = p.head_dim >> 3;
+    const u64 total = (u64)n * p.n_kv * vpr;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        u32 c = (u32)(idx % vpr);
+        u64 t = idx / vpr;
+        u32 h = (u32)(t % p.n_kv);
+        u32 i = (u32)(t / p.n_kv);
+        u32 s = src[i], d = dst[i];
+        if (s >= p.cap || d >= p.cap) continue;
+        u64 so = ((u64)h * p.cap + s) * p.head_dim + c * 8;
+        u64 dof = ((u64)h * p.cap + d) * p.head_dim + c * 8;
+        *(uint4 *)(kc + dof) = *(const uint4 *)(kc + so);
+        *(uint4 *)(vc + dof) = *(const uint4 *)(vc + so);
+    }
+}
+
+extern "C" int tl_kv_copy(const tl_kv_layer *layers, uint32_t n_layer,
+                          const uint32_t *src, const uint32_t *dst, uint32_t n,
+                          void *stream) {
+    if (n == 0 || n_layer == 0) return TL_OK;
+    if (!layers || !src || !dst) return tl_fail(TL_EINVAL, "copy: null pointer");
+    for (u32 l0 = 0; l0 < n_layer; l0 += TL_COPY_MAX_LAYERS) {
+        u32 nl = n_layer - l0 < TL_COPY_MAX_LAYERS ? n_layer - l0 : TL_COPY_MAX_LAYERS;
+        CopyParams p;
+        memset(&p, 0, sizeof(p));
+        for (u32 j = 0; j < nl; j++) {
+            const tl_kv_layer *L = &layers[l0 + j];
+            int rc = check_layer(L);
+            if (rc) return rc;
+            if (L->ring) return tl_fail(TL_EINVAL, "copy: ring layers hold no slot rows");
+            if (j == 0) {
+                p.cap = L->cap;
+                p.n_kv = L->n_kv_head;
+                p.head_dim = L->head_dim;
+            } else if (L->cap != p.cap || L->n_kv_head != p.n_kv ||
+                       L->head_dim != p.head_dim) {
+                return tl_fail(TL_EINVAL, "copy: layers differ in shape");
+            }
+            p.k[j] = (u16 *)L->k;
+            p.v[j] = (u16 *)L->v;
+        }
+        u64 total = (u64)n * p.n_kv * (p.head_dim >> 3);
+        u64 blocks = (total + 255) / 256;
+        if (blocks > 2048) blocks = 2048;
+        hipLaunchKernelGGL(kv_copy_kernel, dim3((u32)blocks, nl), dim3(256), 0,
+                           (hipStream_t)stream, p, src, dst, n);
+        HIP_TRY(hipGetLastError());
+    }
+    return TL_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE                                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* One thread per rotated pair.  theta_i and the angle are formed in f32 as
+ * in the reference: NORM t = 1/powf(base, i/rdim) for even i, NEOX
+ * t = 1/powf(base, 2i/rdim); angle = (float)pos * t. */
+__global__ __launch_bounds__(256) void rope_kernel(float *x, u32 rows, u32 row_stride,
+                                                  u32 heads, u32 hdim, u32 rdim,
+                                                  u32 pos, float base, int neox) {
+    const u32 pairs = rdim >> 1;
+    const u64 total = (u64)rows * heads * pairs;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        u32 i = (u32)(idx % pairs);
+        u64 t = idx / pairs;
+        u32 h = (u32)(t % heads);
+        u32 r = (u32)(t / heads);
+        float *bh = x + (u64)r * row_stride + (u64)h * hdim;
+        u32 ia, ib;
+        float th;
+        if (neox) {
+            th = 1.0f / powf(base, (float)(2 * i) / (float)rdim);
+            ia = i;
+            ib = i + pairs;
+        } else {
+            th = 1.0f / powf(base, (float)(2 * i) / (float)rdim);
+            ia = 2 * i;
+            ib = 2 * i + 1;
+        }
+        float ang = (float)(pos + r) * th;
+        float s, c;
+        sincosf(ang, &s, &c);
+        float a = bh[ia], b = bh[ib];
+        bh[ia] = a * c - b * s;
+        bh[ib] = a * s + b * c;
+    }
+}
+
+extern "C" int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t heads,
+                       uint32_t head_dim, uint32_t rope_dim, uint32_t pos, float theta,
+                       int neox, void *stream) {
+    if (rows == 0) return TL_OK;
+    if (!x || rope_dim > head_dim || (rope_dim & 1) || row_stride < heads * head_dim)
+        return tl_fail(TL_EINVAL, "rope: bad shape");
+    u64 total = (u64)rows * heads * (rope_dim >> 1);
+    u64 blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(rope_kernel, dim3((u32)blocks), dim3(256), 0, (hipStream_t)stream,
+                       x, rows, row_stride, heads, head_dim, rope_dim, pos, theta, neox);
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* split-K decode attention                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* D = head_dim, G = q-heads per kv-head.  256 threads = 4 waves.
+ * A key row (D f16 = D*2 bytes) is read by LPR = D/8 lanes, 16 bytes each,
+ * so one wave load instruction covers KPW = 64/LPR whole rows.  Each lane
+ * group (the LPR lanes of one row position) keeps its own online-softmax
+ * state (m, l, acc[8 dims]) for every q-head of the group; states are merged
+ * across lane groups with shuffles, across waves through LDS, and across
+ * splits by the last workgroup to finish (atomic counter, LSE merge). */
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
+    constexpr int LPR = D / 8;
+    constexpr int KPW = 64 / LPR;
+    constexpr int S = (G <= 4) ? 8 : 4;        /* steps per batch */
+    constexpr int KB = KPW * S;                /* keys per wave batch */
+    constexpr int TILE = 4 * KB;               /* keys per workgroup pass */
+    constexpr float NEG_INF = -__builtin_huge_valf();
+
+    __shared__ float s_acc[4][G][D];
+    __shared__ float s_m[4][G];
+    __shared__ float s_l[4][G];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const u32 grow = blockIdx.z;
+    const u32 si = grow / p.rows_per_seq;
+    const u32 r = grow % p.rows_per_seq;
+    const DecSeq sq = p.seq[si];
+    const u32 kvh = blockIdx.y;
+    const u32 split = blockIdx.x;
+
+    const u32 n_keys = sq.pos + r + 1;
+    const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
+    const u32 kbeg = start + split * p.chunk;
+    const u32 kend = min(kbeg + p.chunk, n_keys);
+
+    const int c = lane % LPR;
+    const int rg = lane / LPR;
+
+    float qr[G][8];
+    const float *qbase = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D + c * 8;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float4 a = *(const float4 *)(qbase + h * D);
+        float4 b = *(const float4 *)(qbase + h * D + 4);
+        qr[h][0] = a.x * p.scale_log2; qr[h][1] = a.y * p.scale_log2;
+        qr[h][2] = a.z * p.scale_log2; qr[h][3] = a.w * p.scale_log2;
+        qr[h][4] = b.x * p.scale_log2; qr[h][5] = b.y * p.scale_log2;
+        qr[h][6] = b.z * p.scale_log2; qr[h][7] = b.w * p.scale_log2;
+    }
+
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        m[h] = NEG_INF;
+        l[h] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[h][j] = 0.f;
+    }
+
+    const u16 *Kh = sq.k + (u64)kvh * sq.cap * D + c * 8;
+    const u16 *Vh = sq.v + (u64)kvh * sq.cap * D + c * 8;
+
+    for (u32 base = kbeg + wave * KB; base < kend; base += TILE) {
+        uint4 kv[S], vv[S];
+        bool ok[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            u32 key = base + s * KPW + rg;
+            ok[s] = key < kend;
+            u32 slot = phys_row(ok[s] ? key : kbeg, sq.ring, sq.slots);
+            if (slot >= sq.cap) { slot = 0; ok[s] = false; }
+            kv[s] = *(const uint4 *)(Kh + (u64)slot * D);
+            vv[s] = *(const uint4 *)(Vh + (u64)slot * D);
+        }
+        float sc[S][G];
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const u32 w[4] = {kv[s].x, kv[s].y, kv[s].z, kv[s].w};
+            float kf[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                kf[2 * j] = f16lo(w[j]);
+                kf[2 * j + 1] = f16hi(w[j]);
+            }
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                float d = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) d = fmaf(qr[h][j], kf[j], d);
+                d = group_sum<LPR>(d);
+                sc[s][h] = ok[s] ? d : NEG_INF;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float mb = sc[0][h];
+#pragma unroll
+            for (int s = 1; s < S; s++) mb = fmaxf(mb, sc[s][h]);
+            float mn = fmaxf(m[h], mb);
+            float mu = (mn == NEG_INF) ? 0.f : mn;
+            float alpha = exp2f(m[h] - mu);
+            m[h] = mn;
+            l[h] *= alpha;
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[h][j] *= alpha;
+#pragma unroll
+            for (int s = 0; s < S; s++) sc[s][h] = exp2f(sc[s][h] - mu);
+        }
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const u32 w[4] = {ok[s] ? vv[s].x : 0u, ok[s] ? vv[s].y : 0u,
+                              ok[s] ? vv[s].z : 0u, ok[s] ? vv[s].w : 0u};
+            float vf[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                vf[2 * j] = f16lo(w[j]);
+                vf[2 * j + 1] = f16hi(w[j]);
+            }
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                float pp = sc[s][h];
+                l[h] += pp;
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc[h][j] = fmaf(pp, vf[j], acc[h][j]);
+            }
+        }
+    }
+
+    /* merge the KPW lane-group states of this wave */
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float mm = m[h];
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+        float mu = (mm == NEG_INF) ? 0.f : mm;
+        float f = exp2f(m[h] - mu);
+        float ll = l[h] * f;
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) ll += __shfl_xor(ll, off);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float a = acc[h][j] * f;
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) a += __shfl_xor(a, off);
+            acc[h][j] = a;
+        }
+        if (rg == 0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) s_acc[wave][h][c * 8 + j] = acc[h][j];
+        }
+        if (lane == 0) {
+            s_m[wave][h] = mm;
+            s_l[wave][h] = ll;
+        }
+    }
+    __syncthreads();
+
+    /* merge the 4 waves; write the final row or this split's partial */
+    const bool single = (p.n_split == 1);
+    for (int o = tid; o < G * D; o += 256) {
+        const int h = o / D, d = o % D;
+        float mm = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
+        float mu = (mm == NEG_INF) ? 0.f : mm;
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            float f = exp2f(s_m[w][h] - mu);
+            L += s_l[w][h] * f;
+            O += s_acc[w][h][d] * f;
+        }
+        const u32 hq = kvh * G + h;
+        if (single) {
+            sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] = O / L;
+        } else {
+            u64 pi = ((u64)grow * p.n_head + hq) * p.n_split + split;
+            p.ws_acc[pi * D + d] = O;
+            if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
+        }
+    }
+    if (single) return;
+
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        u32 old = atomicAdd(&p.counters[(u64)grow * p.n_kv + kvh], 1u);
+        s_last = (old == p.n_split - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    for (int o = tid; o < G * D; o += 256) {
+        const int h = o / D, d = o % D;
+        const u32 hq = kvh * G + h;
+        const u64 pb = ((u64)grow * p.n_head + hq) * p.n_split;
+        float mm = NEG_INF;
+        for (u32 s = 0; s < p.n_split; s++) mm = fmaxf(mm, p.ws_ml[pb + s].x);
+        float mu = (mm == NEG_INF) ? 0.f : mm;
+        float L = 0.f, O = 0.f;
+        for (u32 s = 0; s < p.n_split; s++) {
+            float2 ml = p.ws_ml[pb + s];
+            float f = exp2f(ml.x - mu);
+            L += ml.y * f;
+            O += p.ws_acc[(pb + s) * D + d] * f;
+        }
+        sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] = O / L;
+    }
+    if (tid == 0) p.counters[(u64)grow * p.n_kv + kvh] = 0;
+}
+
+template <int D>
+static int launch_decode_d(const DecParams &p, int G, dim3 grid, hipStream_t st) {
+    switch (G) {
+#define TL_CASE(g)                                                                 \
+    case g:                                                                        \
+        hipLaunchKernelGGL((attn_decode_kernel<D, g>), grid, dim3(256), 0, st, p); \
+        break;
+        TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
+        TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
+#undef TL_CASE
+    default:
+        return tl_fail(TL_EINVAL, "gqa ratio %d unsupported (1..8)", G);
+    }
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+static u32 env_u32(const char *name, u32 dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    return (u32)strtoul(s, NULL, 10);
+}
+
+/* Pick the split count and launch.  max_vis = most visible keys of any row. */
+int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
+                     u32 max_vis, hipStream_t st) {
+    const u32 lpr = head_dim / 8, kpw = 64 / lpr;
+    const u32 S = (G <= 4) ? 8 : 4;
+    const u32 tile = 4 * kpw * S;
+    const u32 target = env_u32("TL_DECODE_WGS", 1024);
+    u64 base_wgs = (u64)n_rows_total * p.n_kv;
+    u32 want = (u32)((target + base_wgs - 1) / base_wgs);
+    u32 max_split = (max_vis + tile - 1) / tile;
+    if (want > max_split) want = max_split;
+    if (want < 1) want = 1;
+    u32 chunk = (max_vis + want - 1) / want;
+    chunk = (chunk + tile - 1) / tile * tile;
+    u32 n_split = (max_vis + chunk - 1) / chunk;
+    p.chunk = chunk;
+    p.n_split = n_split;
+    if (n_split > 1) {
+        TlWorkspace *w;
+        size_t parts = (size_t)n_rows_total * p.n_head * n_split;
+        int rc = tl_workspace_get(parts * head_dim, parts, (size_t)n_rows_total * p.n_kv, &w);
+        if (rc) return rc;
+        p.ws_acc = w->acc;
+        p.ws_ml = (float2 *)w->ml;
+        p.counters = w->cnt;
+    }
+    dim3 grid(n_split, p.n_kv, n_rows_total);
+    switch (head_dim) {
+    case 64: return launch_decode_d<64>(p, (int)G, grid, st);
+    case 128: return launch_decode_d<128>(p, (int)G, grid, st);
+    case 256: return launch_decode_d<256>(p, (int)G, grid, st);
+    default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* OP_ATTN entry points                                                      */
+/* ------------------------------------------------------------------------ */
+
+static int check_args(const tl_kv_layer *L, const tl_attn_args *a) {
+    int rc = check_layer(L);
+    if (rc) return rc;
+    if (!a || !a->q || !a->dst) return tl_fail(TL_EINVAL, "attn: null q/dst");
+    if (a->n_head == 0 || a->n_head % L->n_kv_head)
+        return tl_fail(TL_EINVAL, "attn: n_head %u not a multiple of n_kv %u",
+                       a->n_head, L->n_kv_head);
+    if (a->n_head / L->n_kv_head > 8)
+        return tl_fail(TL_EINVAL, "attn: gqa ratio %u > 8", a->n_head / L->n_kv_head);
+    if (a->q_stride < a->n_head * L->head_dim || (a->q_stride & 3) ||
+        (((uintptr_t)a->q | (uintptr_t)a->dst) & 15))
+        return tl_fail(TL_EINVAL, "attn: q/dst rows must be 16-byte aligned");
+    if (L->ring) {
+        if (!a->window || L->ring < a->window + a->n - 1)
+            return tl_fail(TL_EINVAL, "attn: ring %u too small for window %u and %u rows",
+                           L->ring, a->window, a->n);
+    } else if (!a->slots && (u64)a->pos + a->n > L->cap) {
+        return tl_fail(TL_ERANGE, "attn: pos %u + n %u exceeds cap %u", a->pos, a->n, L->cap);
+    }
+    return TL_OK;
+}
+
+static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st) {
+    DecParams p;
+    memset(&p, 0, sizeof(p));
+    p.seq[0].k = (const u16 *)L->k;
+    p.seq[0].v = (const u16 *)L->v;
+    p.seq[0].slots = a->slots;
+    p.seq[0].q = a->q;
+    p.seq[0].dst = a->dst;
+    p.seq[0].cap = L->cap;
+    p.seq[0].ring = L->ring;
+    p.seq[0].pos = a->pos;
+    p.rows_per_seq = a->n;
+    p.n_kv = L->n_kv_head;
+    p.n_head = a->n_head;
+    p.q_stride = a->q_stride;
+    p.window = a->window;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    u32 max_keys = a->pos + a->n;
+    u32 max_vis = (a->window && max_keys > a->window) ? a->window : max_keys;
+    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(L, a))
+        return tl_launch_prefill(L, a, st);
+    return tl_launch_decode(p, a->n, L->head_dim, a->n_head / L->n_kv_head, max_vis, st);
+}
+
+extern "C" int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
+    int rc = check_args(L, a);
+    if (rc) return rc;
+    if (a->n == 0) return TL_OK;
+    AppendParams ap;
+    memset(&ap, 0, sizeof(ap));
+    rc = fill_seg(ap.seg[0], L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
+    if (rc) return rc;
+    rc = tl_launch_append(ap, 1, (hipStream_t)stream);
+    if (rc) return rc;
+    return attn_core(L, a, (hipStream_t)stream);
+}
+
+extern "C" int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
+    int rc = check_args(L, a);
+    if (rc) return rc;
+    if (a->n == 0) return TL_OK;
+    return attn_core(L, a, (hipStream_t)stream);
+}
+
+extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
+                                    uint32_t n_head, uint32_t window, float scale,
+                                    void *stream) {
+    if (n_seq == 0) return TL_OK;
+    if (!seqs || n_seq > TL_MAX_BATCH_SEQ)
+        return tl_fail(TL_EINVAL, "decode_batch: 1..%d sessions", TL_MAX_BATCH_SEQ);
+    const tl_kv_layer *L0 = &seqs[0].layer;
+    AppendParams ap;
+    memset(&ap, 0, sizeof(ap));
+    DecParams p;
+    memset(&p, 0, sizeof(p));
+    u32 max_vis = 1;
+    for (u32 i = 0; i < n_seq; i++) {
+        const tl_decode_seq *s = &seqs[i];
+        tl_attn_args a;
+        memset(&a, 0, sizeof(a));
+        a.q = s->q; a.k = s->k; a.v = s->v; a.dst = s->dst; a.slots = s->slots;
+        a.pos = s->pos; a.n = 1; a.n_head = n_head;
+        a.q_stride = n_head * s->layer.head_dim;
+        a.kv_stride = s->layer.n_kv_head * s->layer.head_dim;
+        a.window = window; a.scale = scale;
+        int rc = check_args(&s->layer, &a);
+        if (rc) return rc;
+        if (s->layer.n_kv_head != L0->n_kv_head || s->layer.head_dim != L0->head_dim)
+            return tl_fail(TL_EINVAL, "decode_batch: sessions differ in shape");
+        rc = fill_seg(ap.seg[i], &s->layer, s->k, s->v, a.kv_stride, s->slots, s->pos, 1);
+        if (rc) return rc;
+        p.seq[i].k = (const u16 *)s->layer.k;
+        p.seq[i].v = (const u16 *)s->layer.v;
+        p.seq[i].slots = s->slots;
+        p.seq[i].q = s->q;
+        p.seq[i].dst = s->dst;
+        p.seq[i].cap = s->layer.cap;
+        p.seq[i].ring = s->layer.ring;
+        p.seq[i].pos = s->pos;
+        u32 nk = s->pos + 1;
+        u32 vis = (window && nk > window) ? window : nk;
+        if (vis > max_vis) max_vis = vis;
+    }
+    int rc = tl_launch_append(ap, n_seq, (hipStream_t)stream);
+    if (rc) return rc;
+    p.rows_per_seq = 1;
+    p.n_kv = L0->n_kv_head;
+    p.n_head = n_head;
+    p.q_stride = n_head * L0->head_dim;
+    p.window = window;
+    p.scale_log2 = scale * 1.4426950408889634f;
+    return tl_launch_decode(p, n_seq, L0->head_dim, n_head / L0->n_kv_head, max_vis,
+                            (hipStream_t)stream);
+}
