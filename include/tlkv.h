@@ -145,6 +145,13 @@ int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t heads,
             uint32_t head_dim, uint32_t rope_dim, uint32_t pos, float theta,
             int neox, void *stream);
 
+/* Measurement aid (no reference counterpart): stream `bytes` of device
+ * memory with 16-byte loads, `depth` (1/4/8/16) in flight per lane, over
+ * `blocks` workgroups of 256; sink receives blocks*256 words.  Gives the
+ * achievable HBM read ceiling the decode roofline is compared with. */
+int tl_probe_read(const void *src, uint64_t bytes, uint32_t *sink,
+                  uint32_t blocks, uint32_t depth, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -259,7 +259,8 @@ def test_attn_closed_form_identical_keys(T):
 
 
 def test_split_count_invariance(T):
-    """The split-K decomposition does not change the result beyond rounding."""
+    """The split-K decomposition does not change the result beyond rounding
+    (p is rounded to f16 against each tile's running max)."""
     outs = []
     for wgs in ("1", "64", "4096"):
         os.environ["TL_DECODE_WGS"] = wgs
@@ -269,8 +270,8 @@ def test_split_count_invariance(T):
             del os.environ["TL_DECODE_WGS"]
         assert np.abs(out - o16).max() < TOL
         outs.append(out)
-    assert np.abs(outs[0] - outs[1]).max() < 1e-5
-    assert np.abs(outs[0] - outs[2]).max() < 1e-5
+    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+    assert np.abs(outs[0] - outs[2]).max() < 1e-4
 
 
 def test_decode_batch_sessions(T):

@@ -25,6 +25,12 @@ TL_DEV u32 pack_f16x2(float lo, float hi) {
     return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
 }
 
+/* RNE pack without the NaN pinning (operands of dot products). */
+TL_DEV u32 pack_f16x2_fast(float lo, float hi) {
+    return (u32)__builtin_bit_cast(u16, (_Float16)lo) |
+           ((u32)__builtin_bit_cast(u16, (_Float16)hi) << 16);
+}
+
 TL_DEV float f16lo(u32 w) {
     return (float)__builtin_bit_cast(_Float16, (u16)(w & 0xffffu));
 }
@@ -43,14 +49,29 @@ TL_DEV float dpp_f(float x) {
 #define DPP_ROW_HMIRROR 0x141 /* lane i <- lane 7-i within 8 */
 #define DPP_ROW_MIRROR  0x140 /* lane i <- lane 15-i within 16 */
 
-/* Sum over groups of LPR consecutive lanes (LPR in {8,16,32}); every lane of
- * the group receives the group total. */
-template <int LPR>
+/* Sum over aligned groups of N consecutive lanes (N in 1..64, power of 2);
+ * every lane of a group receives the group total.  Within 16 lanes the moves
+ * are DPP (quad_perm xor1/xor2, row_half_mirror, row_mirror: after the quad
+ * steps every lane of a quad holds the quad sum, so the mirrors add the other
+ * quad / half); across rows they are shuffles. */
+template <int N>
 TL_DEV float group_sum(float x) {
-    x += dpp_f<DPP_QUAD_XOR1>(x);
-    x += dpp_f<DPP_QUAD_XOR2>(x);
-    x += dpp_f<DPP_ROW_HMIRROR>(x);
-    if constexpr (LPR >= 16) x += dpp_f<DPP_ROW_MIRROR>(x);
-    if constexpr (LPR >= 32) x += __shfl_xor(x, 16);
+    if constexpr (N >= 2) x += dpp_f<DPP_QUAD_XOR1>(x);
+    if constexpr (N >= 4) x += dpp_f<DPP_QUAD_XOR2>(x);
+    if constexpr (N >= 8) x += dpp_f<DPP_ROW_HMIRROR>(x);
+    if constexpr (N >= 16) x += dpp_f<DPP_ROW_MIRROR>(x);
+    if constexpr (N >= 32) x += __shfl_xor(x, 16);
+    if constexpr (N >= 64) x += __shfl_xor(x, 32);
+    return x;
+}
+
+template <int N>
+TL_DEV float group_max(float x) {
+    if constexpr (N >= 2) x = fmaxf(x, dpp_f<DPP_QUAD_XOR1>(x));
+    if constexpr (N >= 4) x = fmaxf(x, dpp_f<DPP_QUAD_XOR2>(x));
+    if constexpr (N >= 8) x = fmaxf(x, dpp_f<DPP_ROW_HMIRROR>(x));
+    if constexpr (N >= 16) x = fmaxf(x, dpp_f<DPP_ROW_MIRROR>(x));
+    if constexpr (N >= 32) x = fmaxf(x, __shfl_xor(x, 16));
+    if constexpr (N >= 64) x = fmaxf(x, __shfl_xor(x, 32));
     return x;
 }

@@ -30,7 +30,8 @@ struct DecSeq {
     const uint32_t *slots;
     const float *q;
     float *dst;
-    uint32_t cap, ring, pos;
+    const float *kin, *vin;   /* new rows (f32) to append in the same launch, or NULL */
+    uint32_t cap, ring, pos, kv_stride;
 };
 struct DecParams {
     DecSeq seq[TL_MAX_BATCH_SEQ];
@@ -38,9 +39,8 @@ struct DecParams {
     uint32_t n_kv, n_head, q_stride, window;
     float scale_log2;
     uint32_t chunk, n_split;
-    float *ws_acc;
-    float2 *ws_ml;
-    uint32_t *counters;
+    float *ws_acc;           /* split partials: [rows][n_head][n_split][D] */
+    float2 *ws_ml;           /* split (max, sum): [rows][n_head][n_split] */
 };
 
 struct TlWorkspace {
@@ -51,6 +51,16 @@ struct TlWorkspace {
 };
 
 int tl_fail(int code, const char *fmt, ...);
+
+#define HIP_TRY(expr)                                                         \
+    do {                                                                      \
+        hipError_t e_ = (expr);                                               \
+        if (e_ != hipSuccess)                                                 \
+            return tl_fail(TL_EHIP, "%s: %s", #expr, hipGetErrorString(e_));  \
+    } while (0)
+
+/* Most keys one decode workgroup handles (its slot indices are staged in LDS). */
+#define TL_DEC_MAX_CHUNK 2048
 int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters, TlWorkspace **out);
 int tl_launch_append(const AppendParams &p, uint32_t n_seg, hipStream_t stream);
 int tl_launch_decode(DecParams &p, uint32_t n_rows_total, uint32_t head_dim, uint32_t G,

@@ -41,12 +41,6 @@ int tl_fail(int code, const char *fmt, ...) {
 
 extern "C" const char *tl_last_error(void) { return g_err; }
 
-#define HIP_TRY(expr)                                                         \
-    do {                                                                      \
-        hipError_t e_ = (expr);                                               \
-        if (e_ != hipSuccess)                                                 \
-            return tl_fail(TL_EHIP, "%s: %s", #expr, hipGetErrorString(e_));  \
-    } while (0)
 
 /* ------------------------------------------------------------------------ */
 /* per-device workspace for split-K partials                                 */
@@ -393,279 +387,6 @@ extern "C" int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t he
 }
 
 /* ------------------------------------------------------------------------ */
-/* split-K decode attention                                                  */
-/* ------------------------------------------------------------------------ */
-
-/* D = head_dim, G = q-heads per kv-head.  256 threads = 4 waves.
- * A key row (D f16 = D*2 bytes) is read by LPR = D/8 lanes, 16 bytes each,
- * so one wave load instruction covers KPW = 64/LPR whole rows.  Each lane
- * group (the LPR lanes of one row position) keeps its own online-softmax
- * state (m, l, acc[8 dims]) for every q-head of the group; states are merged
- * across lane groups with shuffles, across waves through LDS, and across
- * splits by the last workgroup to finish (atomic counter, LSE merge). */
-template <int D, int G>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
-    constexpr int LPR = D / 8;
-    constexpr int KPW = 64 / LPR;
-    constexpr int S = (G <= 4) ? 8 : 4;        /* steps per batch */
-    constexpr int KB = KPW * S;                /* keys per wave batch */
-    constexpr int TILE = 4 * KB;               /* keys per workgroup pass */
-    constexpr float NEG_INF = -__builtin_huge_valf();
-
-    __shared__ float s_acc[4][G][D];
-    __shared__ float s_m[4][G];
-    __shared__ float s_l[4][G];
-    __shared__ int s_last;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const u32 grow = blockIdx.z;
-    const u32 si = grow / p.rows_per_seq;
-    const u32 r = grow % p.rows_per_seq;
-    const DecSeq sq = p.seq[si];
-    const u32 kvh = blockIdx.y;
-    const u32 split = blockIdx.x;
-
-    const u32 n_keys = sq.pos + r + 1;
-    const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
-    const u32 kbeg = start + split * p.chunk;
-    const u32 kend = min(kbeg + p.chunk, n_keys);
-
-    const int c = lane % LPR;
-    const int rg = lane / LPR;
-
-    float qr[G][8];
-    const float *qbase = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D + c * 8;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        float4 a = *(const float4 *)(qbase + h * D);
-        float4 b = *(const float4 *)(qbase + h * D + 4);
-        qr[h][0] = a.x * p.scale_log2; qr[h][1] = a.y * p.scale_log2;
-        qr[h][2] = a.z * p.scale_log2; qr[h][3] = a.w * p.scale_log2;
-        qr[h][4] = b.x * p.scale_log2; qr[h][5] = b.y * p.scale_log2;
-        qr[h][6] = b.z * p.scale_log2; qr[h][7] = b.w * p.scale_log2;
-    }
-
-    float m[G], l[G], acc[G][8];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        m[h] = NEG_INF;
-        l[h] = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc[h][j] = 0.f;
-    }
-
-    const u16 *Kh = sq.k + (u64)kvh * sq.cap * D + c * 8;
-    const u16 *Vh = sq.v + (u64)kvh * sq.cap * D + c * 8;
-
-    for (u32 base = kbeg + wave * KB; base < kend; base += TILE) {
-        uint4 kv[S], vv[S];
-        bool ok[S];
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            u32 key = base + s * KPW + rg;
-            ok[s] = key < kend;
-            u32 slot = phys_row(ok[s] ? key : kbeg, sq.ring, sq.slots);
-            if (slot >= sq.cap) { slot = 0; ok[s] = false; }
-            kv[s] = *(const uint4 *)(Kh + (u64)slot * D);
-            vv[s] = *(const uint4 *)(Vh + (u64)slot * D);
-        }
-        float sc[S][G];
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            const u32 w[4] = {kv[s].x, kv[s].y, kv[s].z, kv[s].w};
-            float kf[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                kf[2 * j] = f16lo(w[j]);
-                kf[2 * j + 1] = f16hi(w[j]);
-            }
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-                float d = 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) d = fmaf(qr[h][j], kf[j], d);
-                d = group_sum<LPR>(d);
-                sc[s][h] = ok[s] ? d : NEG_INF;
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            float mb = sc[0][h];
-#pragma unroll
-            for (int s = 1; s < S; s++) mb = fmaxf(mb, sc[s][h]);
-            float mn = fmaxf(m[h], mb);
-            float mu = (mn == NEG_INF) ? 0.f : mn;
-            float alpha = exp2f(m[h] - mu);
-            m[h] = mn;
-            l[h] *= alpha;
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[h][j] *= alpha;
-#pragma unroll
-            for (int s = 0; s < S; s++) sc[s][h] = exp2f(sc[s][h] - mu);
-        }
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            const u32 w[4] = {ok[s] ? vv[s].x : 0u, ok[s] ? vv[s].y : 0u,
-                              ok[s] ? vv[s].z : 0u, ok[s] ? vv[s].w : 0u};
-            float vf[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                vf[2 * j] = f16lo(w[j]);
-                vf[2 * j + 1] = f16hi(w[j]);
-            }
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-                float pp = sc[s][h];
-                l[h] += pp;
-#pragma unroll
-                for (int j = 0; j < 8; j++) acc[h][j] = fmaf(pp, vf[j], acc[h][j]);
-            }
-        }
-    }
-
-    /* merge the KPW lane-group states of this wave */
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        float mm = m[h];
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
-        float mu = (mm == NEG_INF) ? 0.f : mm;
-        float f = exp2f(m[h] - mu);
-        float ll = l[h] * f;
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) ll += __shfl_xor(ll, off);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            float a = acc[h][j] * f;
-#pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) a += __shfl_xor(a, off);
-            acc[h][j] = a;
-        }
-        if (rg == 0) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) s_acc[wave][h][c * 8 + j] = acc[h][j];
-        }
-        if (lane == 0) {
-            s_m[wave][h] = mm;
-            s_l[wave][h] = ll;
-        }
-    }
-    __syncthreads();
-
-    /* merge the 4 waves; write the final row or this split's partial */
-    const bool single = (p.n_split == 1);
-    for (int o = tid; o < G * D; o += 256) {
-        const int h = o / D, d = o % D;
-        float mm = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
-        float mu = (mm == NEG_INF) ? 0.f : mm;
-        float L = 0.f, O = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            float f = exp2f(s_m[w][h] - mu);
-            L += s_l[w][h] * f;
-            O += s_acc[w][h][d] * f;
-        }
-        const u32 hq = kvh * G + h;
-        if (single) {
-            sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] = O / L;
-        } else {
-            u64 pi = ((u64)grow * p.n_head + hq) * p.n_split + split;
-            p.ws_acc[pi * D + d] = O;
-            if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
-        }
-    }
-    if (single) return;
-
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        u32 old = atomicAdd(&p.counters[(u64)grow * p.n_kv + kvh], 1u);
-        s_last = (old == p.n_split - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    for (int o = tid; o < G * D; o += 256) {
-        const int h = o / D, d = o % D;
-        const u32 hq = kvh * G + h;
-        const u64 pb = ((u64)grow * p.n_head + hq) * p.n_split;
-        float mm = NEG_INF;
-        for (u32 s = 0; s < p.n_split; s++) mm = fmaxf(mm, p.ws_ml[pb + s].x);
-        float mu = (mm == NEG_INF) ? 0.f : mm;
-        float L = 0.f, O = 0.f;
-        for (u32 s = 0; s < p.n_split; s++) {
-            float2 ml = p.ws_ml[pb + s];
-            float f = exp2f(ml.x - mu);
-            L += ml.y * f;
-            O += p.ws_acc[(pb + s) * D + d] * f;
-        }
-        sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] = O / L;
-    }
-    if (tid == 0) p.counters[(u64)grow * p.n_kv + kvh] = 0;
-}
-
-template <int D>
-static int launch_decode_d(const DecParams &p, int G, dim3 grid, hipStream_t st) {
-    switch (G) {
-#define TL_CASE(g)                                                                 \
-    case g:                                                                        \
-        hipLaunchKernelGGL((attn_decode_kernel<D, g>), grid, dim3(256), 0, st, p); \
-        break;
-        TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
-        TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
-#undef TL_CASE
-    default:
-        return tl_fail(TL_EINVAL, "gqa ratio %d unsupported (1..8)", G);
-    }
-    HIP_TRY(hipGetLastError());
-    return TL_OK;
-}
-
-static u32 env_u32(const char *name, u32 dflt) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    return (u32)strtoul(s, NULL, 10);
-}
-
-/* Pick the split count and launch.  max_vis = most visible keys of any row. */
-int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
-                     u32 max_vis, hipStream_t st) {
-    const u32 lpr = head_dim / 8, kpw = 64 / lpr;
-    const u32 S = (G <= 4) ? 8 : 4;
-    const u32 tile = 4 * kpw * S;
-    const u32 target = env_u32("TL_DECODE_WGS", 1024);
-    u64 base_wgs = (u64)n_rows_total * p.n_kv;
-    u32 want = (u32)((target + base_wgs - 1) / base_wgs);
-    u32 max_split = (max_vis + tile - 1) / tile;
-    if (want > max_split) want = max_split;
-    if (want < 1) want = 1;
-    u32 chunk = (max_vis + want - 1) / want;
-    chunk = (chunk + tile - 1) / tile * tile;
-    u32 n_split = (max_vis + chunk - 1) / chunk;
-    p.chunk = chunk;
-    p.n_split = n_split;
-    if (n_split > 1) {
-        TlWorkspace *w;
-        size_t parts = (size_t)n_rows_total * p.n_head * n_split;
-        int rc = tl_workspace_get(parts * head_dim, parts, (size_t)n_rows_total * p.n_kv, &w);
-        if (rc) return rc;
-        p.ws_acc = w->acc;
-        p.ws_ml = (float2 *)w->ml;
-        p.counters = w->cnt;
-    }
-    dim3 grid(n_split, p.n_kv, n_rows_total);
-    switch (head_dim) {
-    case 64: return launch_decode_d<64>(p, (int)G, grid, st);
-    case 128: return launch_decode_d<128>(p, (int)G, grid, st);
-    case 256: return launch_decode_d<256>(p, (int)G, grid, st);
-    default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
-    }
-}
-
-/* ------------------------------------------------------------------------ */
 /* OP_ATTN entry points                                                      */
 /* ------------------------------------------------------------------------ */
 
@@ -691,9 +412,32 @@ static int check_args(const tl_kv_layer *L, const tl_attn_args *a) {
     return TL_OK;
 }
 
-static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st) {
+/* append (when `append`) + attention.  Decode-sized batches run as one
+ * fused launch (the decode kernel writes the new rows itself); prefill-sized
+ * ones append first and then run the MFMA kernel. */
+static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
+                     hipStream_t st) {
+    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(L, a)) {
+        if (append) {
+            AppendParams ap;
+            memset(&ap, 0, sizeof(ap));
+            int rc = fill_seg(ap.seg[0], L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
+            if (rc) return rc;
+            rc = tl_launch_append(ap, 1, st);
+            if (rc) return rc;
+        }
+        return tl_launch_prefill(L, a, st);
+    }
     DecParams p;
     memset(&p, 0, sizeof(p));
+    if (append) {
+        AppendSeg chk;
+        int rc = fill_seg(chk, L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
+        if (rc) return rc;
+        p.seq[0].kin = a->k;
+        p.seq[0].vin = a->v;
+        p.seq[0].kv_stride = a->kv_stride;
+    }
     p.seq[0].k = (const u16 *)L->k;
     p.seq[0].v = (const u16 *)L->v;
     p.seq[0].slots = a->slots;
@@ -710,8 +454,6 @@ static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st
     p.scale_log2 = a->scale * 1.4426950408889634f;
     u32 max_keys = a->pos + a->n;
     u32 max_vis = (a->window && max_keys > a->window) ? a->window : max_keys;
-    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(L, a))
-        return tl_launch_prefill(L, a, st);
     return tl_launch_decode(p, a->n, L->head_dim, a->n_head / L->n_kv_head, max_vis, st);
 }
 
@@ -719,20 +461,14 @@ extern "C" int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream
     int rc = check_args(L, a);
     if (rc) return rc;
     if (a->n == 0) return TL_OK;
-    AppendParams ap;
-    memset(&ap, 0, sizeof(ap));
-    rc = fill_seg(ap.seg[0], L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
-    if (rc) return rc;
-    rc = tl_launch_append(ap, 1, (hipStream_t)stream);
-    if (rc) return rc;
-    return attn_core(L, a, (hipStream_t)stream);
+    return attn_core(L, a, true, (hipStream_t)stream);
 }
 
 extern "C" int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
     int rc = check_args(L, a);
     if (rc) return rc;
     if (a->n == 0) return TL_OK;
-    return attn_core(L, a, (hipStream_t)stream);
+    return attn_core(L, a, false, (hipStream_t)stream);
 }
 
 extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
@@ -742,8 +478,6 @@ extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
     if (!seqs || n_seq > TL_MAX_BATCH_SEQ)
         return tl_fail(TL_EINVAL, "decode_batch: 1..%d sessions", TL_MAX_BATCH_SEQ);
     const tl_kv_layer *L0 = &seqs[0].layer;
-    AppendParams ap;
-    memset(&ap, 0, sizeof(ap));
     DecParams p;
     memset(&p, 0, sizeof(p));
     u32 max_vis = 1;
@@ -760,8 +494,12 @@ extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
         if (rc) return rc;
         if (s->layer.n_kv_head != L0->n_kv_head || s->layer.head_dim != L0->head_dim)
             return tl_fail(TL_EINVAL, "decode_batch: sessions differ in shape");
-        rc = fill_seg(ap.seg[i], &s->layer, s->k, s->v, a.kv_stride, s->slots, s->pos, 1);
+        AppendSeg chk;
+        rc = fill_seg(chk, &s->layer, s->k, s->v, a.kv_stride, s->slots, s->pos, 1);
         if (rc) return rc;
+        p.seq[i].kin = s->k;
+        p.seq[i].vin = s->v;
+        p.seq[i].kv_stride = a.kv_stride;
         p.seq[i].k = (const u16 *)s->layer.k;
         p.seq[i].v = (const u16 *)s->layer.v;
         p.seq[i].slots = s->slots;
@@ -774,8 +512,6 @@ extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
         u32 vis = (window && nk > window) ? window : nk;
         if (vis > max_vis) max_vis = vis;
     }
-    int rc = tl_launch_append(ap, n_seq, (hipStream_t)stream);
-    if (rc) return rc;
     p.rows_per_seq = 1;
     p.n_kv = L0->n_kv_head;
     p.n_head = n_head;
@@ -784,4 +520,45 @@ extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
     p.scale_log2 = scale * 1.4426950408889634f;
     return tl_launch_decode(p, n_seq, L0->head_dim, n_head / L0->n_kv_head, max_vis,
                             (hipStream_t)stream);
+}
+
+/* ------------------------------------------------------------------------ */
+/* HBM read-bandwidth probe (measurement aid)                                */
+/* ------------------------------------------------------------------------ */
+
+/* Streams `bytes` from src with 16-byte loads, `depth` independent loads in
+ * flight per lane, and writes one word per thread so the loads stay live. */
+template <int DEPTH>
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4 *src, u64 n16, u32 *sink) {
+    u32 acc = 0;
+    const u64 stride = (u64)gridDim.x * blockDim.x;
+    u64 i = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + (DEPTH - 1) * stride < n16; i += DEPTH * stride) {
+        uint4 v[DEPTH];
+#pragma unroll
+        for (int k = 0; k < DEPTH; k++) v[k] = src[i + k * stride];
+#pragma unroll
+        for (int k = 0; k < DEPTH; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < n16; i += stride) {
+        uint4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    sink[(u64)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+extern "C" int tl_probe_read(const void *src, uint64_t bytes, uint32_t *sink,
+                             uint32_t blocks, uint32_t depth, void *stream) {
+    if (!src || !sink || (bytes & 15) || blocks == 0)
+        return tl_fail(TL_EINVAL, "probe: bad arguments");
+    const u64 n16 = bytes / 16;
+    switch (depth) {
+    case 1: hipLaunchKernelGGL(read_probe_kernel<1>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4 *)src, n16, sink); break;
+    case 4: hipLaunchKernelGGL(read_probe_kernel<4>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4 *)src, n16, sink); break;
+    case 8: hipLaunchKernelGGL(read_probe_kernel<8>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4 *)src, n16, sink); break;
+    case 16: hipLaunchKernelGGL(read_probe_kernel<16>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4 *)src, n16, sink); break;
+    default: return tl_fail(TL_EINVAL, "probe: depth 1/4/8/16");
+    }
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
 }

@@ -63,6 +63,7 @@ def lib():
                                  ctypes.c_float, vp],
         "tl_rope": [vp, u32, u32, u32, u32, u32, u32, ctypes.c_float,
                     ctypes.c_int, vp],
+        "tl_probe_read": [vp, ctypes.c_uint64, vp, u32, u32, vp],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
