@@ -1,0 +1,119 @@
+/*
+ * tl_kvcache.h — host-side KV-cache bookkeeping: the prefix cache that maps a
+ * request's logical positions to physical cache rows ("slots").
+ *
+ * Drop-in for the reference's src/kvcache.h:72-90 — same function names,
+ * signatures and semantics:
+ *   kv_cache_create      src/kvcache.c:122-174  (slot 0 pops first, all free)
+ *   kv_cache_destroy     src/kvcache.c:176-190
+ *   kv_cache_match       src/kvcache.c:192-218  (lock the longest cached prefix)
+ *   kv_cache_append      src/kvcache.c:220-270  (map / allocate slots for
+ *                        [pos, pos+n); LRU leaf eviction when the pool is empty,
+ *                        src/kvcache.c:70-120)
+ *   kv_cache_checkpoint  src/kvcache.c:272-300  (recurrent-state snapshots)
+ *   kv_cache_restore     src/kvcache.c:302-321
+ * The request map (req.slots / req.len / req.shared_len / req.active), the
+ * per-slot metadata and the statistics keep the reference's field names, so
+ * code that reads radix->req.slots (src/backend/cpu/cpu_op.c:988-993) reads
+ * the same thing here.
+ *
+ * Differences that callers can observe: none in slot assignment, eviction
+ * order, hit counts or return values (checked against the compiled reference
+ * on random request streams).  The prefix index is a token trie instead of
+ * the vendored rax; eviction picks the same victim (the in-tree leaf with
+ * ref_count 0 and the smallest last_used) from a heap instead of a full scan.
+ * Session and KvCache are opaque here: kv_cache_create only keeps the
+ * pointers; state snapshots go through the callbacks set with
+ * tl_kv_cache_set_state_ops (none set = no snapshots, as for a Session whose
+ * graph has no recurrent state).
+ */
+#ifndef TL_KVCACHE_H
+#define TL_KVCACHE_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint32_t u32;
+typedef uint64_t u64;
+
+typedef struct Session Session;   /* opaque: passed back to the state callbacks */
+typedef struct KvCache KvCache;   /* opaque: only stored */
+
+#define KV_SLOT_NONE UINT32_MAX
+
+typedef struct {
+    u32  token;        /* token id stored in this slot */
+    u32  parent;       /* slot of the previous token; KV_SLOT_NONE for root */
+    u32  child_count;  /* direct children (leaf detection) */
+    u32  ref_count;    /* requests currently using this slot */
+    u64  last_used;    /* LRU clock value */
+    u32  snap;         /* state snapshot index or KV_SLOT_NONE */
+    bool in_tree;      /* attached to the prefix index */
+} KvSlotMeta;
+
+typedef struct {
+    u32  n_slots;
+    u32  n_free;
+    u32 *free_stack;   /* LIFO of free slot indices */
+} KvSlotPool;
+
+typedef struct {
+    u32 *slots;        /* [ctx_size] logical position -> physical slot */
+    u32  len;
+    u32  shared_len;
+    bool active;
+} KvRequestState;
+
+typedef struct {
+    u64 hit_tokens;
+    u64 computed_tokens;
+    u64 evictions;
+    u64 allocations;
+} KvRequstStats;       /* spelled as the reference spells it (kvcache.h:34-39) */
+
+typedef struct {
+    void *state;
+    u32   slot;
+    u32   pos;
+    u64   last_used;
+    bool  valid;
+} KvStateSnapshot;
+
+/* Recurrent-state callbacks (the reference calls graph_state_bytes/save/load,
+ * src/graph.c:368-408). */
+typedef struct {
+    size_t (*bytes)(Session *s);
+    bool   (*save)(Session *s, void *dst, size_t cap);
+    bool   (*load)(Session *s, const void *src, size_t len);
+} TlKvStateOps;
+
+typedef struct KvRadixCache KvRadixCache;
+
+KvRadixCache *kv_cache_create(Session *s, KvCache *kv, u32 ctx_size);
+void kv_cache_destroy(KvRadixCache *c);
+u32  kv_cache_match(KvRadixCache *c, const u32 *tokens, u32 n);
+bool kv_cache_append(KvRadixCache *c, const u32 *tokens, u32 pos, u32 n);
+bool kv_cache_checkpoint(KvRadixCache *c, u32 pos);
+u32  kv_cache_restore(KvRadixCache *c, u32 matched, u32 n, bool *restored);
+
+/* ---- accessors (no reference counterpart: the reference's callers read the
+ *      struct fields directly) ---- */
+void tl_kv_cache_set_state_ops(KvRadixCache *c, const TlKvStateOps *ops);
+const KvRequestState *tl_kv_cache_req(const KvRadixCache *c);
+const KvRequstStats  *tl_kv_cache_stats(const KvRadixCache *c);
+const KvSlotMeta     *tl_kv_cache_meta(const KvRadixCache *c, u32 slot);
+u32  tl_kv_cache_n_free(const KvRadixCache *c);
+u64  tl_kv_cache_clock(const KvRadixCache *c);
+/* Lowest req.slots index written since the last call (KV_SLOT_NONE if none),
+ * and reset; lets a device mirror of req.slots upload only what changed. */
+u32  tl_kv_cache_take_dirty(KvRadixCache *c);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,73 @@
+/*
+ * tl_session.h — the KV part of the reference's executor for one session:
+ * KV storage per layer on the device, the prefix cache on the host, a device
+ * mirror of the request's slot table, and the micro-batch loop that runs
+ * OP_ATTN for every layer.
+ *
+ * Counterparts in the reference:
+ *   tl_session_create     cache_build_attn_kvcache, src/graph.c:817-872
+ *                         (per-layer K/V storage sized ctx_size, radix created
+ *                         with kv_cache_create(s, kc, ctx_size))
+ *   tl_session_kv_prepare graph_kv_prepare, src/graph.c:1423-1454, for the
+ *                         stateless (rewindable) architectures: match, reset,
+ *                         resume = matched < n ? matched : matched - 1
+ *                         (0 when nothing matched); the caller then sets the
+ *                         position to `resume` as server.c:834-837 does
+ *   tl_session_execute    graph_execute, src/graph.c:1360-1421, restricted to
+ *                         the KV path: n_ubatch chunks, kv_cache_append per
+ *                         chunk ("KV slot allocation failed" -> TL_ERANGE),
+ *                         then OP_ATTN on every layer with the chunk's rows
+ *
+ * The activations that the rest of the model would produce (RoPE'd Q and K,
+ * V) are inputs: per layer a device array [n_tokens][stride] f32.  Output is
+ * the attention result per layer, [n_tokens][q_stride] f32.
+ */
+#ifndef TL_SESSION_H
+#define TL_SESSION_H
+
+#include <stdint.h>
+#include "tlkv.h"
+#include "tl_kvcache.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tl_session tl_session;
+
+typedef struct tl_session_cfg {
+    uint32_t        n_layer;
+    uint32_t        n_head;       /* q heads */
+    uint32_t        n_kv_head;
+    uint32_t        head_dim;     /* == kv_head_dim */
+    uint32_t        ctx_size;     /* KV pool size in rows (Session.ctx_size) */
+    uint32_t        n_ubatch;     /* prefill chunk (Session.n_ubatch) */
+    const uint32_t *window;       /* [n_layer] sliding window (0 = full) or NULL */
+    const uint32_t *ring;         /* [n_layer] ring rows for windowed layers
+                                     (0 = addressed through the slot table) or NULL */
+    int             use_radix;    /* 1: prefix cache maps positions to slots */
+    void           *stream;       /* hipStream_t, NULL = default stream */
+} tl_session_cfg;
+
+int  tl_session_create(const tl_session_cfg *cfg, tl_session **out);
+void tl_session_destroy(tl_session *s);
+
+int  tl_session_kv_prepare(tl_session *s, const uint32_t *tokens, uint32_t n,
+                           uint32_t *matched, uint32_t *resume);
+
+int  tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
+                        const float *const *q, const float *const *k,
+                        const float *const *v, float *const *out,
+                        uint32_t q_stride, uint32_t kv_stride);
+
+/* accessors */
+uint32_t           tl_session_pos(const tl_session *s);        /* Session.n_tokens */
+void               tl_session_set_pos(tl_session *s, uint32_t pos);
+KvRadixCache      *tl_session_radix(tl_session *s);            /* NULL without radix */
+const tl_kv_layer *tl_session_layer(const tl_session *s, uint32_t layer);
+const uint32_t    *tl_session_device_slots(const tl_session *s);  /* device [ctx_size] */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,149 @@
+"""Write the golden vectors under tests/golden/ from the COMPILED REFERENCE
+(oracle/_ref/libtlref.so, built by `make -C oracle` from the reference's own
+sources).  Run here, where the reference tree exists:
+
+    python tests/golden/make_golden.py
+
+Fixtures (numpy .npz, no pickles):
+  kvcache_trace.npz  kv_cache_match / kv_cache_append op streams over small
+                     pools (heavy LRU eviction) and the reference's state after
+                     every op: return value, req.len, req.shared_len,
+                     req.active, pool.n_free, stats, clock, req.slots[0..len).
+  op_attn.npz        cpu_graph_op(OP_ATTN) outputs over an f32 cache for tiny
+                     GQA / window / slot-table cases (inputs included).
+  rope.npz           cpu_graph_op(OP_ROPE_NORM / OP_ROPE_NEOX) outputs.
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+import oracle as O  # noqa: E402
+
+
+def kv_streams():
+    """Op streams: (ctx, list of ops); op = ('m', tokens) or ('a', tokens, pos, n)."""
+    out = []
+    for seed, ctx, n_req, vocab in ((1, 48, 60, 40), (2, 96, 80, 500), (3, 32, 40, 8)):
+        rng = np.random.default_rng(seed)
+        prefixes = [rng.integers(0, vocab, size=rng.integers(3, ctx // 2)) for _ in range(4)]
+        ops = []
+        for _ in range(n_req):
+            toks = np.concatenate([prefixes[rng.integers(len(prefixes))],
+                                   rng.integers(0, vocab, size=rng.integers(1, ctx // 3))])
+            toks = toks[:ctx].astype(np.uint32)
+            ops.append(("m", toks))
+            # resume rule of graph_kv_prepare, then chunked appends
+            ops.append(("prep", toks))
+        out.append((ctx, ops, seed))
+    return out
+
+
+def gen_kvcache():
+    rec_ops, rec_tok, rec_state, rec_slots, rec_stream = [], [], [], [], []
+    tok_off = 0
+    slot_off = 0
+    for si, (ctx, ops, seed) in enumerate(kv_streams()):
+        rng = np.random.default_rng(seed + 100)
+        kv = O.RefKv(ctx)
+        for op in ops:
+            toks = op[1]
+            if op[0] == "m":
+                calls = [("m", 0, 0)]
+            else:
+                m = last_match
+                pos = 0 if m == 0 else (m if m < len(toks) else m - 1)
+                calls = []
+                while pos < len(toks):
+                    n = int(min(rng.integers(1, 9), len(toks) - pos))
+                    calls.append(("a", pos, n))
+                    pos += n
+            for kind, pos, n in calls:
+                if kind == "m":
+                    ret = kv.match(toks)
+                    last_match = ret
+                else:
+                    ret = int(kv.append(toks, pos, n))
+                r = kv.req()
+                st = kv.stats()
+                sl = kv.slots(r["len"])
+                rec_ops.append([si, 0 if kind == "m" else 1, tok_off, len(toks), pos, n])
+                rec_state.append([ret, r["len"], r["shared_len"], int(r["active"]), r["n_free"],
+                                  st["hit_tokens"], st["computed_tokens"], st["evictions"],
+                                  st["allocations"], st["clock"], slot_off, len(sl)])
+                rec_slots.append(sl)
+                slot_off += len(sl)
+                if kind == "a" and not ret:
+                    break
+            rec_tok.append(toks)
+            tok_off += len(toks)
+        rec_stream.append(ctx)
+    np.savez_compressed(os.path.join(HERE, "kvcache_trace.npz"),
+                        ctx=np.array(rec_stream, dtype=np.uint32),
+                        ops=np.array(rec_ops, dtype=np.int64),
+                        tokens=np.concatenate(rec_tok).astype(np.uint32),
+                        state=np.array(rec_state, dtype=np.uint64),
+                        slots=np.concatenate(rec_slots).astype(np.uint32))
+
+
+ATTN_CASES = [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted
+    (4, 2, 64, 24, 0, 1, 0, False),
+    (4, 2, 64, 24, 9, 1, 0, True),
+    (8, 2, 64, 40, 5, 7, 0, True),
+    (8, 2, 64, 40, 5, 7, 3, True),
+    (8, 8, 128, 20, 11, 2, 0, False),
+    (6, 2, 128, 33, 17, 4, 8, True),
+    (4, 4, 256, 16, 6, 3, 0, True),
+    (8, 4, 256, 16, 6, 3, 4, False),
+]
+
+
+def gen_attn():
+    arrays = {}
+    for ci, (nh, nkv, hd, cap, pos, n, win, perm) in enumerate(ATTN_CASES):
+        rng = np.random.default_rng(1000 + ci)
+        kc = rng.standard_normal((nkv, cap, hd), dtype=np.float32)
+        vc = rng.standard_normal((nkv, cap, hd), dtype=np.float32)
+        q = rng.standard_normal((n, nh * hd), dtype=np.float32)
+        k = rng.standard_normal((n, nkv * hd), dtype=np.float32)
+        v = rng.standard_normal((n, nkv * hd), dtype=np.float32)
+        slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+        out = O.ref_attn(kc.copy(), vc.copy(), q, k, v, slots if perm else None, pos, n, nh, win)
+        meta = np.array([nh, nkv, hd, cap, pos, n, win, int(perm)], dtype=np.int64)
+        for name, a in (("meta", meta), ("kc", kc), ("vc", vc), ("q", q), ("k", k), ("v", v),
+                        ("slots", slots), ("out", out)):
+            arrays[f"c{ci}_{name}"] = a
+    arrays["n_cases"] = np.array(len(ATTN_CASES))
+    np.savez_compressed(os.path.join(HERE, "op_attn.npz"), **arrays)
+
+
+def gen_rope():
+    arrays = {}
+    cases = [(0, 4, 64, 64, 0, 500000.0), (0, 8, 128, 128, 32000, 500000.0),
+             (1, 4, 128, 128, 777, 1e6), (1, 2, 256, 256, 16000, 10000.0),
+             (1, 2, 256, 64, 300, 1e6)]
+    for ci, (neox, heads, hd, rd, pos, theta) in enumerate(cases):
+        rng = np.random.default_rng(2000 + ci)
+        x = rng.standard_normal((5, heads * hd), dtype=np.float32)
+        y = O.ref_rope(x, heads, hd, rd, pos, theta, neox)
+        arrays[f"c{ci}_meta"] = np.array([neox, heads, hd, rd, pos], dtype=np.int64)
+        arrays[f"c{ci}_theta"] = np.array(theta, dtype=np.float32)
+        arrays[f"c{ci}_x"] = x
+        arrays[f"c{ci}_y"] = y
+    arrays["n_cases"] = np.array(len(cases))
+    np.savez_compressed(os.path.join(HERE, "rope.npz"), **arrays)
+
+
+if __name__ == "__main__":
+    if not O.ref_available():
+        O.build()
+    if not O.ref_available():
+        sys.exit("the compiled reference (oracle/_ref) is not available")
+    gen_kvcache()
+    gen_attn()
+    gen_rope()
+    print("golden vectors written to", HERE)

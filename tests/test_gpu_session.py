@@ -1,0 +1,116 @@
+"""The session layer on the GPU: prefix cache (kv_cache_*) + device slot-table
+mirror + micro-batch loop + fused OP_ATTN, checked against the oracle.
+
+K/V rows are a deterministic function of the token prefix (as a model's
+would be), so a reused prefix holds exactly the rows a recomputation would
+write.  Each request's outputs must match the oracle's op_attn over a
+contiguous f16 cache holding that request's own rows, within 2e-3; the cache
+contents behind the request's slot map must be bit-exact f16 of its rows.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def T():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import tlkv
+    tlkv.check(tlkv.lib().tl_init(0))
+    return torch
+
+
+def prefix_rows(tokens, p, width, salt):
+    """K or V row of position p: a function of tokens[0..p] only."""
+    h = hashlib.blake2b(np.asarray(tokens[:p + 1], np.uint32).tobytes() + salt, digest_size=8)
+    rng = np.random.default_rng(int.from_bytes(h.digest(), "little"))
+    return rng.standard_normal(width).astype(np.float32)
+
+
+def run_session(T, n_layer, nh, nkv, hd, ctx, ub, prompts, decode_steps, window=None,
+                ring=None, seed=0):
+    import tlkv
+    S = tlkv.Session(n_layer, nh, nkv, hd, ctx, ub, window=window, ring=ring)
+    rng = np.random.default_rng(seed)
+    qd, kd = nh * hd, nkv * hd
+    results = []
+    for pi, prompt in enumerate(prompts):
+        full = list(prompt) + [int(x) for x in rng.integers(0, 1000, size=decode_steps)]
+        matched, resume = S.kv_prepare(np.array(prompt, np.uint32))
+        calls = [(resume, len(prompt))] + [(p, p + 1) for p in range(len(prompt), len(full))]
+        outs = []
+        for (a, b) in calls:
+            toks = np.array(full[a:b], np.uint32)
+            n = b - a
+            q = [rng.standard_normal((n, qd)).astype(np.float32) for _ in range(n_layer)]
+            k = [np.stack([prefix_rows(full, p, kd, b"k%d" % l) for p in range(a, b)])
+                 for l in range(n_layer)]
+            v = [np.stack([prefix_rows(full, p, kd, b"v%d" % l) for p in range(a, b)])
+                 for l in range(n_layer)]
+            dq = [T.from_numpy(x).cuda() for x in q]
+            dk = [T.from_numpy(x).cuda() for x in k]
+            dv = [T.from_numpy(x).cuda() for x in v]
+            do = [T.zeros((n, qd), dtype=T.float32, device="cuda") for _ in range(n_layer)]
+            S.execute(toks, dq, dk, dv, do, qd, kd)
+            T.cuda.synchronize()
+            outs.append((a, b, q, [x.cpu().numpy() for x in do]))
+        # oracle: the request's own rows in a contiguous f16 cache
+        for l in range(n_layer):
+            C = O.Cache(len(full), nkv, hd)
+            allk = np.stack([prefix_rows(full, p, kd, b"k%d" % l) for p in range(len(full))])
+            allv = np.stack([prefix_rows(full, p, kd, b"v%d" % l) for p in range(len(full))])
+            C.append(allk[:outs[0][0]], allv[:outs[0][0]], None, 0, outs[0][0])
+            win = window[l] if window else 0
+            for (a, b, q, o) in outs:
+                ref = O.attn(C, q[l], allk[a:b], allv[a:b], None, a, b - a, nh, window=win)
+                err = np.abs(o[l] - ref).max()
+                assert err < TOL, f"prompt {pi} layer {l} rows {a}:{b} err {err}"
+            # slot-mapped cache rows are the request's rows, bit for bit
+            if not (ring and ring[l]):
+                slots = T.from_numpy(S.radix_slots(len(full))).cuda()
+                ko = T.zeros((len(full), nkv, hd), dtype=T.float16, device="cuda")
+                vo = T.zeros_like(ko)
+                L = S.layer(l)
+                tlkv.check(tlkv.lib().tl_kv_gather(L, tlkv.ptr(slots), len(full),
+                                                   tlkv.ptr(ko), tlkv.ptr(vo), None))
+                T.cuda.synchronize()
+                assert np.array_equal(ko.cpu().numpy().view(np.uint16).reshape(len(full), -1),
+                                      O.f16_bits(allk))
+                assert np.array_equal(vo.cpu().numpy().view(np.uint16).reshape(len(full), -1),
+                                      O.f16_bits(allv))
+        results.append((matched, resume))
+    return S, results
+
+
+def test_session_prefix_reuse_and_eviction(T):
+    rng = np.random.default_rng(1)
+    shared = [list(rng.integers(0, 1000, size=n)) for n in (20, 33)]
+    prompts = []
+    for i in range(6):
+        prompts.append(shared[i % 2] + list(rng.integers(0, 1000, size=5 + i)))
+    prompts.append(list(prompts[-1]))         # full hit: last token recomputed
+    S, res = run_session(T, 2, 8, 2, 128, 96, 16, prompts, decode_steps=3)
+    matched = [m for m, _ in res]
+    assert matched[0] == 0 and matched[2] >= 20 and matched[3] >= 33
+    assert res[-1][0] == len(prompts[-1]) and res[-1][1] == len(prompts[-1]) - 1
+
+
+def test_session_gqa7_multi_chunk(T):
+    rng = np.random.default_rng(2)
+    prompts = [list(rng.integers(0, 151936, size=70)), list(rng.integers(0, 151936, size=40))]
+    run_session(T, 2, 28, 4, 128, 256, 32, prompts, decode_steps=2, seed=3)
+
+
+def test_session_window_ring_layer(T):
+    rng = np.random.default_rng(3)
+    prompts = [list(rng.integers(0, 1000, size=50))]
+    # layer 0 windowed on a ring of win + ub - 1 rows, layer 1 global
+    run_session(T, 2, 8, 4, 256, 128, 8, prompts, decode_steps=4, window=[16, 0],
+                ring=[16 + 8 - 1, 0], seed=4)

@@ -562,3 +562,6 @@ extern "C" int tl_probe_read(const void *src, uint64_t bytes, uint32_t *sink,
     HIP_TRY(hipGetLastError());
     return TL_OK;
 }
+
+/* Error reporting for the C translation units of the library. */
+extern "C" int tl_set_error(int code, const char *msg) { return tl_fail(code, "%s", msg); }

@@ -114,3 +114,192 @@ def attn_args(q, k, v, dst, slots, pos, n, n_head, head_dim, n_kv, window,
                     None if v is None else v.data_ptr(), dst.data_ptr(),
                     None if slots is None else slots.data_ptr(), pos, n, n_head,
                     n_head * head_dim, n_kv * head_dim, window, scale)
+
+
+# ---- host KV bookkeeping (include/tl_kvcache.h) ------------------------------
+
+class KvSlotMeta(ctypes.Structure):
+    _fields_ = [("token", u32), ("parent", u32), ("child_count", u32),
+                ("ref_count", u32), ("last_used", ctypes.c_uint64), ("snap", u32),
+                ("in_tree", ctypes.c_bool)]
+
+
+class KvRequestState(ctypes.Structure):
+    _fields_ = [("slots", ctypes.POINTER(u32)), ("len", u32), ("shared_len", u32),
+                ("active", ctypes.c_bool)]
+
+
+class KvRequstStats(ctypes.Structure):
+    _fields_ = [("hit_tokens", ctypes.c_uint64), ("computed_tokens", ctypes.c_uint64),
+                ("evictions", ctypes.c_uint64), ("allocations", ctypes.c_uint64)]
+
+
+_kv_sigs_done = False
+
+
+def _kv_sigs():
+    global _kv_sigs_done
+    L = lib()
+    if _kv_sigs_done:
+        return L
+    u32p = ctypes.POINTER(u32)
+    L.kv_cache_create.argtypes = [vp, vp, u32]
+    L.kv_cache_create.restype = vp
+    L.kv_cache_destroy.argtypes = [vp]
+    L.kv_cache_destroy.restype = None
+    L.kv_cache_match.argtypes = [vp, u32p, u32]
+    L.kv_cache_match.restype = u32
+    L.kv_cache_append.argtypes = [vp, u32p, u32, u32]
+    L.kv_cache_append.restype = ctypes.c_bool
+    L.tl_kv_cache_req.argtypes = [vp]
+    L.tl_kv_cache_req.restype = ctypes.POINTER(KvRequestState)
+    L.tl_kv_cache_stats.argtypes = [vp]
+    L.tl_kv_cache_stats.restype = ctypes.POINTER(KvRequstStats)
+    L.tl_kv_cache_meta.argtypes = [vp, u32]
+    L.tl_kv_cache_meta.restype = ctypes.POINTER(KvSlotMeta)
+    L.tl_kv_cache_n_free.argtypes = [vp]
+    L.tl_kv_cache_n_free.restype = u32
+    L.tl_kv_cache_clock.argtypes = [vp]
+    L.tl_kv_cache_clock.restype = ctypes.c_uint64
+    L.tl_kv_cache_take_dirty.argtypes = [vp]
+    L.tl_kv_cache_take_dirty.restype = u32
+    _kv_sigs_done = True
+    return L
+
+
+def _u32_array(tokens):
+    import numpy as np
+    a = np.ascontiguousarray(tokens, dtype=np.uint32)
+    return a, a.ctypes.data_as(ctypes.POINTER(u32))
+
+
+class KvCache:
+    """kv_cache_* of libtlkv (the product's host prefix cache)."""
+
+    def __init__(self, ctx):
+        self.L = _kv_sigs()
+        self._dummy = ctypes.c_uint32(1)          # stands for the opaque KvCache*
+        self.h = self.L.kv_cache_create(None, ctypes.addressof(self._dummy), ctx)
+        if not self.h:
+            raise TlError("kv_cache_create failed")
+        self.ctx = ctx
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.kv_cache_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def match(self, tokens):
+        a, p = _u32_array(tokens)
+        return int(self.L.kv_cache_match(self.h, p, a.size))
+
+    def append(self, tokens, pos, n):
+        a, p = _u32_array(tokens)
+        return bool(self.L.kv_cache_append(self.h, p, pos, n))
+
+    def req(self):
+        r = self.L.tl_kv_cache_req(self.h).contents
+        return dict(len=int(r.len), shared_len=int(r.shared_len), active=bool(r.active),
+                    n_free=int(self.L.tl_kv_cache_n_free(self.h)))
+
+    def slots(self, n=None):
+        import numpy as np
+        n = self.ctx if n is None else n
+        r = self.L.tl_kv_cache_req(self.h).contents
+        return np.ctypeslib.as_array(r.slots, shape=(self.ctx,))[:n].copy()
+
+    def stats(self):
+        s = self.L.tl_kv_cache_stats(self.h).contents
+        return dict(hit_tokens=int(s.hit_tokens), computed_tokens=int(s.computed_tokens),
+                    evictions=int(s.evictions), allocations=int(s.allocations),
+                    clock=int(self.L.tl_kv_cache_clock(self.h)))
+
+    def meta(self, slot):
+        m = self.L.tl_kv_cache_meta(self.h, slot).contents
+        return dict(token=int(m.token), parent=int(m.parent), child_count=int(m.child_count),
+                    ref_count=int(m.ref_count), in_tree=bool(m.in_tree),
+                    last_used=int(m.last_used))
+
+    def take_dirty(self):
+        return int(self.L.tl_kv_cache_take_dirty(self.h))
+
+
+# ---- session (include/tl_session.h) -------------------------------------------
+
+class SessionCfg(ctypes.Structure):
+    _fields_ = [("n_layer", u32), ("n_head", u32), ("n_kv_head", u32), ("head_dim", u32),
+                ("ctx_size", u32), ("n_ubatch", u32), ("window", ctypes.POINTER(u32)),
+                ("ring", ctypes.POINTER(u32)), ("use_radix", ctypes.c_int),
+                ("stream", vp)]
+
+
+class Session:
+    """tl_session: device KV storage + host prefix cache + micro-batch loop."""
+
+    def __init__(self, n_layer, n_head, n_kv_head, head_dim, ctx_size, n_ubatch,
+                 window=None, ring=None, use_radix=True, stream=None):
+        L = lib()
+        if not getattr(L, "_sess_sigs", False):
+            L.tl_session_create.argtypes = [ctypes.POINTER(SessionCfg), ctypes.POINTER(vp)]
+            L.tl_session_create.restype = ctypes.c_int
+            L.tl_session_destroy.argtypes = [vp]
+            L.tl_session_destroy.restype = None
+            L.tl_session_kv_prepare.argtypes = [vp, ctypes.POINTER(u32), u32,
+                                                ctypes.POINTER(u32), ctypes.POINTER(u32)]
+            L.tl_session_kv_prepare.restype = ctypes.c_int
+            L.tl_session_execute.argtypes = [vp, ctypes.POINTER(u32), u32,
+                                             ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                             ctypes.POINTER(vp), ctypes.POINTER(vp), u32, u32]
+            L.tl_session_execute.restype = ctypes.c_int
+            L.tl_session_pos.argtypes = [vp]
+            L.tl_session_pos.restype = u32
+            L.tl_session_radix.argtypes = [vp]
+            L.tl_session_radix.restype = vp
+            L.tl_session_layer.argtypes = [vp, u32]
+            L.tl_session_layer.restype = ctypes.POINTER(KvLayer)
+            L._sess_sigs = True
+        self.L = L
+        self.n_layer = n_layer
+        self._win = (u32 * n_layer)(*(window or [0] * n_layer))
+        self._ring = (u32 * n_layer)(*(ring or [0] * n_layer))
+        cfg = SessionCfg(n_layer, n_head, n_kv_head, head_dim, ctx_size, n_ubatch,
+                         self._win, self._ring, int(use_radix),
+                         None if stream is None else stream)
+        h = vp()
+        check(L.tl_session_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.tl_session_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+    def kv_prepare(self, tokens):
+        a, p = _u32_array(tokens)
+        m, r = u32(), u32()
+        check(self.L.tl_session_kv_prepare(self.h, p, a.size, ctypes.byref(m), ctypes.byref(r)))
+        return int(m.value), int(r.value)
+
+    def execute(self, tokens, q, k, v, out, q_stride, kv_stride):
+        """q/k/v/out: per-layer device tensors [n_tokens][stride]."""
+        a, p = _u32_array(tokens)
+        arr = lambda ts: (vp * self.n_layer)(*[t.data_ptr() for t in ts])
+        check(self.L.tl_session_execute(self.h, p, a.size, arr(q), arr(k), arr(v), arr(out),
+                                        q_stride, kv_stride))
+
+    @property
+    def pos(self):
+        return int(self.L.tl_session_pos(self.h))
+
+    def radix_slots(self, n):
+        import numpy as np
+        r = self.L.tl_session_radix(self.h)
+        req = _kv_sigs().tl_kv_cache_req(r).contents
+        return np.ctypeslib.as_array(req.slots, shape=(n,)).copy()
+
+    def layer(self, l):
+        return self.L.tl_session_layer(self.h, l).contents
