@@ -159,8 +159,22 @@ static void or_softmax(float *x, u32 n) {          /* cpu_op.c:338-349 */
     for (u32 i = 0; i < n; i++) x[i] /= sum;
 }
 
-static inline float cache_at(const void *c, int f16, u64 i) {
-    return f16 ? or_f16_to_f32(((const u16 *)c)[i]) : ((const float *)c)[i];
+/* binary16 -> f32 table (filled from or_f16_to_f32 on first use) */
+static float g_h2f[65536];
+static int g_h2f_ready;
+
+static void h2f_init(void) {
+    if (g_h2f_ready) return;
+    for (u32 i = 0; i < 65536; i++) g_h2f[i] = or_f16_to_f32((u16)i);
+    g_h2f_ready = 1;
+}
+
+/* one cached row as f32 */
+static inline const float *cache_row(const void *c, int f16, u64 off, u32 khd, float *tmp) {
+    if (!f16) return (const float *)c + off;
+    const u16 *h = (const u16 *)c + off;
+    for (u32 d = 0; d < khd; d++) tmp[d] = g_h2f[h[d]];
+    return tmp;
 }
 
 /* op_attn restated: write the batch's K/V rows (converted to the cache
@@ -189,8 +203,14 @@ int or_attn(const float *q, const float *k, const float *v, float *dst,
                             slots, pos, n)) {
         return -1;
     }
+    h2f_init();
     float *scr = (float *)malloc(((size_t)pos + n) * sizeof(float));
-    if (!scr) return -2;
+    float *row = (float *)malloc((size_t)khd * sizeof(float));
+    if (!scr || !row) {
+        free(scr);
+        free(row);
+        return -2;
+    }
     memset(dst, 0, (size_t)n * q_dim * sizeof(float));
     for (u32 h = 0; h < n_head; h++) {
         u32 kv_h = h / gqa;
@@ -202,11 +222,14 @@ int or_attn(const float *q, const float *k, const float *v, float *dst,
             for (u32 t = 0; t < n_vis; t++) {
                 u32 lp = start + t;
                 u32 slot = ring ? lp % ring : (slots ? slots[lp] : lp);
-                if (slot >= cap) { free(scr); return -1; }
-                u64 base = (u64)kv_h * hs + (u64)slot * khd;
+                if (slot >= cap) {
+                    free(scr);
+                    free(row);
+                    return -1;
+                }
+                const float *kr = cache_row(kc, cache_f16, (u64)kv_h * hs + (u64)slot * khd, khd, row);
                 float sum = 0.0f;
-                for (u32 d = 0; d < khd; d++)
-                    sum += cache_at(kc, cache_f16, base + d) * qh[d];
+                for (u32 d = 0; d < khd; d++) sum += kr[d] * qh[d];
                 scr[t] = sum * scale;
             }
             or_softmax(scr, n_vis);
@@ -214,14 +237,14 @@ int or_attn(const float *q, const float *k, const float *v, float *dst,
             for (u32 t = 0; t < n_vis; t++) {
                 u32 lp = start + t;
                 u32 slot = ring ? lp % ring : (slots ? slots[lp] : lp);
-                u64 base = (u64)kv_h * hs + (u64)slot * khd;
+                const float *vr = cache_row(vc, cache_f16, (u64)kv_h * hs + (u64)slot * khd, khd, row);
                 float st = scr[t];
-                for (u32 d = 0; d < khd; d++)
-                    oh[d] += st * cache_at(vc, cache_f16, base + d);
+                for (u32 d = 0; d < khd; d++) oh[d] += st * vr[d];
             }
         }
     }
     free(scr);
+    free(row);
     return 0;
 }
 

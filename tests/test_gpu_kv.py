@@ -322,3 +322,42 @@ def test_rope_vs_oracle(T, neox):
     # angles up to ~3e3 rad: one f32 ulp of the angle is ~2.4e-4 rad; libm
     # (reference: -ffast-math glibc) and the device differ by a few ulp
     assert np.abs(host(dx) - ref).max() < 2e-3
+
+
+PREFILL_CASES = [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted slots
+    (32, 8, 128, 600, 0, 512, 0, False),     # config 4 first chunk
+    (32, 8, 128, 1600, 1000, 512, 0, True),  # config 4 later chunk, slot table
+    (32, 8, 64, 1100, 512, 512, 0, True),    # config 1 shape
+    (28, 4, 128, 700, 300, 100, 0, True),    # gqa 7, ragged rows
+    (8, 4, 256, 800, 600, 64, 128, True),    # config 5 local layer (window)
+    (8, 4, 256, 800, 500, 200, 0, False),    # config 5 global layer
+    (16, 2, 128, 300, 7, 16, 5, True),       # smallest prefill batch, tiny window
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES)
+def test_prefill_vs_oracle(T, case):
+    n_head, n_kv, hd, cap, pos, n, window, perm = case
+    rng = np.random.default_rng(sum(case))
+    slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                    seed=pos + 3 * n)
+    e16 = np.abs(out - o16).max()
+    e32 = np.abs(out - o32).max()
+    assert e16 < TOL, f"vs f16-cache oracle {e16}"
+    assert e32 < TOL, f"vs f32-cache (reference) oracle {e32}"
+
+
+def test_prefill_split_invariance(T):
+    outs = []
+    for ns in ("1", "3", "7"):
+        os.environ["TL_PREFILL_SPLITS"] = ns
+        try:
+            out, o16, _, _, _ = _run_attn(T, 32, 8, 128, 2100, 1500, 512, 0, None, seed=21)
+        finally:
+            del os.environ["TL_PREFILL_SPLITS"]
+        assert np.abs(out - o16).max() < TOL
+        outs.append(out)
+    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+    assert np.abs(outs[0] - outs[2]).max() < 1e-4

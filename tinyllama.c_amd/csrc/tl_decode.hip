@@ -554,11 +554,17 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
     }
     if (rc || n_split == 1) return rc;
+    return tl_launch_merge(p, n_rows_total, head_dim, st);
+}
+
+int tl_launch_merge(const DecParams &p, u32 n_rows_total, u32 head_dim, hipStream_t st) {
+    if (p.n_split > TL_MERGE_MAX_SPLIT) return tl_fail(TL_EINVAL, "merge: %u splits", p.n_split);
     dim3 mg(n_rows_total * p.n_head);
     switch (head_dim) {
     case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(256), 0, st, p); break;
     case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(256), 0, st, p); break;
     case 256: hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(256), 0, st, p); break;
+    default: return tl_fail(TL_EINVAL, "merge: head_dim %u", head_dim);
     }
     HIP_TRY(hipGetLastError());
     return TL_OK;

@@ -43,6 +43,20 @@ struct DecParams {
     float2 *ws_ml;           /* split (max, sum): [rows][n_head][n_split] */
 };
 
+/* Chunked-prefill launch (one OP_ATTN batch of one session). */
+struct PrefParams {
+    const uint16_t *k, *v;
+    const uint32_t *slots;
+    uint32_t cap, ring;
+    const float *q;
+    float *dst;
+    uint32_t q_stride, pos, n, n_head, n_kv, window;
+    float scale_log2;
+    uint32_t n_split;
+    float *ws_acc;
+    float2 *ws_ml;
+};
+
 struct TlWorkspace {
     float *acc;
     float *ml;
@@ -65,6 +79,8 @@ int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters, TlWork
 int tl_launch_append(const AppendParams &p, uint32_t n_seg, hipStream_t stream);
 int tl_launch_decode(DecParams &p, uint32_t n_rows_total, uint32_t head_dim, uint32_t G,
                      uint32_t max_vis, hipStream_t st);
+/* combine n_split partial rows (ws_acc / ws_ml) into seq[..].dst */
+int tl_launch_merge(const DecParams &p, uint32_t n_rows_total, uint32_t head_dim, hipStream_t st);
 
 /* MFMA chunked-prefill attention (tl_prefill.hip). */
 bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a);

@@ -1,9 +1,346 @@
-/* tl_prefill.hip — MFMA chunked-prefill attention (gfx950). */
+/*
+ * tl_prefill.hip — chunked-prefill attention on MFMA (gfx950).
+ *
+ * Math of op_attn (reference src/backend/cpu/cpu_op.c:1011-1062) for a batch
+ * of n rows at positions pos..pos+n-1: row i attends to keys
+ * [start_i, pos+i] (causal, start_i = pos+i+1-window when windowed) through
+ * the slot table; out = softmax(q.K^T * scale) V.
+ *
+ * Work decomposition:
+ *   A workgroup owns one kv-head, a block of 32*QB query rows and one split
+ *   of the key range; its W = G*QB waves each own one q-head of the GQA group
+ *   and 32 query rows, so every K/V tile staged in LDS serves G*QB*32 rows.
+ *   Per 32-key tile:
+ *     S^T[key][row] = K . Q^T      v_mfma_f32_32x32x16_f16, A = K rows from
+ *                                  LDS, B = Q (registers, f16, pre-scaled by
+ *                                  scale*log2 e); each lane ends up owning one
+ *                                  query row and 16 of the tile's keys, so the
+ *                                  row max / sum need one shuffle between the
+ *                                  two half-waves.
+ *     online softmax in f32 (exp2), P^T packed to f16 straight from the
+ *                                  accumulator registers.
+ *     O^T[d][row] += V^T . P^T     v_mfma_f32_32x32x16_f16, A = V^T from LDS
+ *                                  (the tile is stored transposed), B = P^T.
+ *                                  The MFMA's reduction index k is mapped to
+ *                                  the keys each lane already holds, so P^T
+ *                                  never goes through LDS.
+ *   The next tile's K/V rows are loaded into registers while the current one
+ *   is computed.  Key splits (when the grid would not fill the chip) write
+ *   partial (O, max, sum) rows that attn_merge_kernel combines.
+ */
 #include "tl_common.h"
 #include "tl_internal.h"
 
-bool tl_prefill_supported(const tl_kv_layer *, const tl_attn_args *) { return false; }
+#include <stdlib.h>
+#include <string.h>
 
-int tl_launch_prefill(const tl_kv_layer *, const tl_attn_args *, hipStream_t) {
-    return tl_fail(TL_EINVAL, "prefill kernel not available");
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+template <int D, int G>
+struct PCfg {
+    static constexpr int WMAX = (D <= 128) ? 8 : 4;
+    static constexpr int QB = (WMAX / G) > 0 ? (WMAX / G) : 1;   /* 32-row query blocks */
+    static constexpr int W = G * QB;                              /* waves */
+    static constexpr int ROWS = 32 * QB;                          /* query rows per WG */
+};
+
+#define TL_PF_BN 32        /* keys per tile */
+#define TL_PF_VS 36        /* V^T row stride in halves (32 keys + pad) */
+
+TL_DEV half8_t h8_from_u4(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+
+TL_DEV u32 pack2(float a, float b) { return pack_f16x2_fast(a, b); }
+
+template <int D, int G>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * PCfg<D, G>::W))) void attn_prefill_kernel(const PrefParams p) {
+    using C = PCfg<D, G>;
+    constexpr int W = C::W, ROWS = C::ROWS;
+    constexpr int T = 64 * W;
+    constexpr int BN = TL_PF_BN, VS = TL_PF_VS;
+    constexpr int CPR = D / 8;           /* 16-byte chunks per row */
+    constexpr int KS = D / 16;           /* k-steps of the QK MFMA */
+    constexpr int DB = D / 32;           /* 32-row d-blocks of O^T */
+    constexpr int UNITS = BN * CPR;      /* 16-byte units per tile */
+    constexpr int UPT = (UNITS + T - 1) / T;
+    constexpr float NEG_INF = -__builtin_huge_valf();
+
+    __shared__ uint4 s_k[UNITS];
+    __shared__ _Float16 s_vt[D * VS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5;             /* half-wave */
+    const int lr = lane & 31;
+
+    /* block -> (K/V range x = kvh * n_split + split, query block); blocks that
+     * read the same K/V range sit on the same XCD (block b runs on XCD b % 8) */
+    const u32 nx = p.n_kv * p.n_split;
+    const u32 x = blockIdx.x % nx, qblk = blockIdx.x / nx;
+    const u32 kvh = x / p.n_split, split = x % p.n_split;
+
+    const int g = wave % G, qsub = wave / G;
+    const u32 hq = kvh * G + g;
+    const u32 qb0 = qblk * ROWS;
+    const u32 my_q = qb0 + qsub * 32 + lr;           /* lane's query row */
+    const bool row_ok = my_q < p.n;
+    const u32 qpos = p.pos + my_q;
+
+    /* key range of the workgroup, then of this split */
+    const u32 wg_last = min(p.pos + qb0 + ROWS, p.pos + p.n);
+    const u32 first_pos = p.pos + qb0;
+    const u32 wg_first = (p.window && first_pos + 1 > p.window) ? first_pos + 1 - p.window : 0;
+    const u32 span = wg_last - wg_first;
+    u32 chunk = (span + p.n_split - 1) / p.n_split;
+    chunk = (chunk + BN - 1) / BN * BN;
+    const u32 ks = wg_first + split * chunk;
+    const u32 ke = min(ks + chunk, wg_last);
+
+    /* Q operand: lane holds Q[row lr][16s + 8h .. +8], f16, log2-scaled */
+    half8_t qop[KS];
+    {
+        const float *qrow = p.q + (u64)(row_ok ? my_q : 0) * p.q_stride + (u64)hq * D;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const float4 a = *(const float4 *)(qrow + 16 * s + 8 * h);
+            const float4 b = *(const float4 *)(qrow + 16 * s + 8 * h + 4);
+            const float sc = row_ok ? p.scale_log2 : 0.f;
+            uint4 u = make_uint4(pack2(a.x * sc, a.y * sc), pack2(a.z * sc, a.w * sc),
+                                 pack2(b.x * sc, b.y * sc), pack2(b.z * sc, b.w * sc));
+            qop[s] = h8_from_u4(u);
+        }
+    }
+
+    floatx16_t o[DB];
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[b][r] = 0.f;
+    float m = NEG_INF, lsum = 0.f;
+
+    const u16 *Kb = p.k + (u64)kvh * p.cap * D;
+    const u16 *Vb = p.v + (u64)kvh * p.cap * D;
+
+    /* register staging of one tile: unit u = tid + j*T -> row u / CPR,
+     * chunk u % CPR; rows past ke load zeros */
+    uint4 rk[UPT], rv[UPT];
+    auto load_tile = [&](u32 tb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < UPT; j++) {
+            const int u = tid + j * T;
+            const int row = u / CPR, c = u % CPR;
+            const u32 key = tb + row;
+            rk[j] = make_uint4(0, 0, 0, 0);
+            rv[j] = make_uint4(0, 0, 0, 0);
+            if (u < UNITS && key < ke) {
+                u32 ph = p.ring ? key % p.ring : (p.slots ? p.slots[key] : key);
+                ph = ph < p.cap ? ph : 0;
+                rk[j] = *(const uint4 *)(Kb + (u64)ph * D + c * 8);
+                rv[j] = *(const uint4 *)(Vb + (u64)ph * D + c * 8);
+            }
+        }
+    };
+
+    if (ks < ke) load_tile(ks);
+    for (u32 tb = ks; tb < ke; tb += BN) {
+        __syncthreads();                 /* previous tile fully consumed */
+#pragma unroll
+        for (int j = 0; j < UPT; j++) {
+            const int u = tid + j * T;
+            if (u < UNITS) {
+                const int row = u / CPR, c = u % CPR;
+                s_k[row * CPR + (c ^ (row % CPR))] = rk[j];
+                const u32 w[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    s_vt[(c * 8 + 2 * e) * VS + row] = __builtin_bit_cast(_Float16, (u16)(w[e] & 0xffff));
+                    s_vt[(c * 8 + 2 * e + 1) * VS + row] = __builtin_bit_cast(_Float16, (u16)(w[e] >> 16));
+                }
+            }
+        }
+        __syncthreads();
+        if (tb + BN < ke) load_tile(tb + BN);
+
+        /* S^T = K . Q^T : lane holds keys 8(r/4) + 4h + r%4 of query lr */
+        floatx16_t sacc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sacc[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const int c = 2 * s + h;
+            const half8_t a = h8_from_u4(s_k[lr * CPR + (c ^ (lr % CPR))]);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[s], sacc, 0, 0, 0);
+        }
+
+        /* mask + online softmax */
+        float sv[16];
+        float mt = NEG_INF;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const u32 key = tb + 8 * (r / 4) + 4 * h + (r % 4);
+            const bool ok = row_ok && key < ke && key <= qpos &&
+                            (!p.window || key + p.window > qpos);
+            sv[r] = ok ? sacc[r] : NEG_INF;
+            mt = fmaxf(mt, sv[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float mu = (mn == NEG_INF) ? 0.f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - mu);
+        m = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            sv[r] = __builtin_amdgcn_exp2f(sv[r] - mu);
+            ps += sv[r];
+        }
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int b = 0; b < DB; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[b][r] *= alpha;
+
+        /* P^T operands: k = 8h + j maps to the keys this lane holds */
+        const half8_t p0 = h8_from_u4(make_uint4(pack2(sv[0], sv[1]), pack2(sv[2], sv[3]),
+                                                 pack2(sv[4], sv[5]), pack2(sv[6], sv[7])));
+        const half8_t p1 = h8_from_u4(make_uint4(pack2(sv[8], sv[9]), pack2(sv[10], sv[11]),
+                                                 pack2(sv[12], sv[13]), pack2(sv[14], sv[15])));
+
+        /* O^T += V^T . P^T */
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+            const _Float16 *vr = s_vt + (32 * b + lr) * VS;
+            const uint2 x0 = *(const uint2 *)(vr + 4 * h);
+            const uint2 x1 = *(const uint2 *)(vr + 8 + 4 * h);
+            const uint2 y0 = *(const uint2 *)(vr + 16 + 4 * h);
+            const uint2 y1 = *(const uint2 *)(vr + 24 + 4 * h);
+            const half8_t a0 = h8_from_u4(make_uint4(x0.x, x0.y, x1.x, x1.y));
+            const half8_t a1 = h8_from_u4(make_uint4(y0.x, y0.y, y1.x, y1.y));
+            o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, p0, o[b], 0, 0, 0);
+            o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, p1, o[b], 0, 0, 0);
+        }
+    }
+    lsum += __shfl_xor(lsum, 32);
+
+    if (!row_ok) return;
+    /* o[b][r] = O^T[d = 32b + 8(r/4) + 4h + r%4][row lr] */
+    if (p.n_split == 1) {
+        float *dst = p.dst + (u64)my_q * p.q_stride + (u64)hq * D;
+        const float inv = 1.0f / lsum;
+#pragma unroll
+        for (int b = 0; b < DB; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) dst[32 * b + 8 * (r / 4) + 4 * h + (r % 4)] = o[b][r] * inv;
+    } else {
+        const u64 pi = ((u64)my_q * p.n_head + hq) * p.n_split + split;
+        float *acc = p.ws_acc + pi * D;
+#pragma unroll
+        for (int b = 0; b < DB; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[32 * b + 8 * (r / 4) + 4 * h + (r % 4)] = o[b][r];
+        if (h == 0) p.ws_ml[pi] = make_float2(m, lsum);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+
+bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a) {
+    if (getenv("TL_NO_PREFILL")) return false;
+    const u32 G = a->n_head / L->n_kv_head;
+    return (L->head_dim == 64 || L->head_dim == 128 || L->head_dim == 256) && G >= 1 && G <= 8;
+}
+
+template <int D, int G>
+static void launch_pf(const PrefParams &p, u32 blocks, hipStream_t st) {
+    hipLaunchKernelGGL((attn_prefill_kernel<D, G>), dim3(blocks), dim3(64 * PCfg<D, G>::W), 0,
+                       st, p);
+}
+
+template <int D>
+static int launch_pf_d(const PrefParams &p, int G, u32 blocks, hipStream_t st) {
+    switch (G) {
+    case 1: launch_pf<D, 1>(p, blocks, st); break;
+    case 2: launch_pf<D, 2>(p, blocks, st); break;
+    case 3: launch_pf<D, 3>(p, blocks, st); break;
+    case 4: launch_pf<D, 4>(p, blocks, st); break;
+    case 5: launch_pf<D, 5>(p, blocks, st); break;
+    case 6: launch_pf<D, 6>(p, blocks, st); break;
+    case 7: launch_pf<D, 7>(p, blocks, st); break;
+    case 8: launch_pf<D, 8>(p, blocks, st); break;
+    default: return tl_fail(TL_EINVAL, "prefill: gqa %d", G);
+    }
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+static u32 rows_per_wg(u32 D, u32 G) {
+    const u32 wmax = D <= 128 ? 8 : 4;
+    const u32 qb = wmax / G ? wmax / G : 1;
+    return 32 * qb;
+}
+
+int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st) {
+    const u32 D = L->head_dim, G = a->n_head / L->n_kv_head;
+    PrefParams p;
+    memset(&p, 0, sizeof(p));
+    p.k = (const u16 *)L->k;
+    p.v = (const u16 *)L->v;
+    p.slots = a->slots;
+    p.cap = L->cap;
+    p.ring = L->ring;
+    p.q = a->q;
+    p.dst = a->dst;
+    p.q_stride = a->q_stride;
+    p.pos = a->pos;
+    p.n = a->n;
+    p.n_head = a->n_head;
+    p.n_kv = L->n_kv_head;
+    p.window = a->window;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+
+    const u32 rows = rows_per_wg(D, G);
+    const u32 nqb = (a->n + rows - 1) / rows;
+    int cus = 256;
+    {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+    }
+    const u32 base = nqb * L->n_kv_head;
+    const u32 span = a->pos + a->n;        /* most keys any workgroup sees */
+    u32 ns = (u32)((cus + base - 1) / base);
+    const u32 max_ns = (span + 511) / 512;  /* keep >= 512 keys per split */
+    if (ns > max_ns) ns = max_ns;
+    if (ns < 1) ns = 1;
+    if (const char *e = getenv("TL_PREFILL_SPLITS")) ns = (u32)atoi(e) ? (u32)atoi(e) : ns;
+    p.n_split = ns;
+    if (ns > 1) {
+        TlWorkspace *w;
+        size_t parts = (size_t)a->n * a->n_head * ns;
+        int rc = tl_workspace_get(parts * D, parts, 0, &w);
+        if (rc) return rc;
+        p.ws_acc = w->acc;
+        p.ws_ml = (float2 *)w->ml;
+    }
+    const u32 blocks = base * ns;
+    int rc;
+    switch (D) {
+    case 64: rc = launch_pf_d<64>(p, (int)G, blocks, st); break;
+    case 128: rc = launch_pf_d<128>(p, (int)G, blocks, st); break;
+    case 256: rc = launch_pf_d<256>(p, (int)G, blocks, st); break;
+    default: return tl_fail(TL_EINVAL, "prefill: head_dim %u", D);
+    }
+    if (rc || ns == 1) return rc;
+    /* combine the key splits (same partial layout as the decode kernel) */
+    DecParams mp;
+    memset(&mp, 0, sizeof(mp));
+    mp.seq[0].dst = a->dst;
+    mp.rows_per_seq = a->n;
+    mp.n_kv = L->n_kv_head;
+    mp.n_head = a->n_head;
+    mp.q_stride = a->q_stride;
+    mp.n_split = ns;
+    mp.ws_acc = p.ws_acc;
+    mp.ws_ml = p.ws_ml;
+    return tl_launch_merge(mp, a->n, D, st);
 }
