@@ -89,6 +89,19 @@ def cpu_baseline(c, P, n_layers_sample):
                       f"the f16 workload's algorithmic bytes"}
 
 
+def profiled_traffic():
+    """HBM bytes per decode launch pair from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/attn_decode_llama3-8b-32k_hbm_traffic.md)."""
+    path = os.path.join(ROOT, "profiles", "attn_decode_llama3-8b-32k_hbm_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def hbm_read_ceiling(torch, tlkv, lib, sh):
     """Best streaming-read rate of a plain 16-byte-load kernel over 4 GiB."""
     x = torch.empty(2 * 1024 ** 3, dtype=torch.float16, device="cuda")
@@ -275,7 +288,7 @@ def main():
                            "launch (decode.tok_s)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": profiled_traffic(),
                      "kernel": "attn_decode_kernel<128,4> + attn_merge_kernel<128> "
                                "(one OP_ATTN launch pair)"},
     }
