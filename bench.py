@@ -123,6 +123,266 @@ def hbm_read_ceiling(torch, tlkv, lib, sh):
     return best
 
 
+# ---- the other BASELINE configs (reported beside the north star) -------------
+
+def _gbs(nbytes, ms):
+    return nbytes / (ms / 1e3) / 1e9
+
+
+def run_config1(torch, tlkv, lib, sh, gen):
+    """Config 1, Llama-3.2-1B KV (L16 Hq32 Hkv8 d64), 1 slot: one 512-row
+    OP_ATTN chunk (MFMA prefill with fused append), then 256 decode steps of
+    OP_ATTN (fused append + attention) per layer.  RoPE NORM theta 5e5."""
+    c = dict(L=16, Hq=32, Hkv=8, d=64, theta=500000.0)
+    L, Hq, Hkv, d = c["L"], c["Hq"], c["Hkv"], c["d"]
+    kd, qd, ub, steps = Hkv * d, Hq * d, 512, 256
+    cap = ub + steps
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    stream = torch.cuda.current_stream()
+    layers = [tlkv.Layer(cap, Hkv, d) for _ in range(L)]
+    slots = torch.arange(cap, dtype=torch.int32, device="cuda")
+    q = torch.randn((L, ub, qd), generator=gen, device="cuda")
+    k = torch.randn((L, ub, kd), generator=gen, device="cuda")
+    v = torch.randn((L, ub, kd), generator=gen, device="cuda")
+    out = torch.empty((L, ub, qd), device="cuda")
+    for l in range(L):
+        tlkv.check(lib.tl_rope(tlkv.ptr(q[l]), ub, qd, Hq, d, d, 0, c["theta"], 0, sh))
+        tlkv.check(lib.tl_rope(tlkv.ptr(k[l]), ub, kd, Hkv, d, d, 0, c["theta"], 0, sh))
+    e0, e1, e2, e3 = (torch.cuda.Event(enable_timing=True) for _ in range(4))
+    e0.record(stream)
+    for l in range(L):
+        a = tlkv.attn_args(q[l], k[l], v[l], out[l], slots, 0, ub, Hq, d, Hkv, 0, scale)
+        tlkv.check(lib.tl_attn(layers[l].desc, a, sh))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    args_l = [tlkv.attn_args(q[l, :1], k[l, :1], v[l, :1], out[l, :1], slots, 0, 1, Hq, d,
+                             Hkv, 0, scale) for l in range(L)]
+    e2.record(stream)
+    nbytes = 0
+    for s in range(steps):
+        pos = ub + s
+        for l in range(L):
+            args_l[l].pos = pos
+            tlkv.check(lib.tl_attn(layers[l].desc, args_l[l], sh))
+        nbytes += L * decode_bytes(c, pos + 1)
+    e3.record(stream)
+    torch.cuda.synchronize()
+    pf_ms, dec_ms = e0.elapsed_time(e1), e2.elapsed_time(e3)
+    pf_flops = L * prefill_flops(c, 0, ub)
+    return {"workload": "config 1: L16 Hq32 Hkv8 d64, 512-row OP_ATTN chunk then 256 decode "
+                        "steps (fused append + attention)",
+            "prefill_TFLOPs": round(pf_flops / (pf_ms / 1e3) / 1e12, 2),
+            "prefill_ms": round(pf_ms, 3),
+            "decode_GBs": round(_gbs(nbytes, dec_ms), 1),
+            "decode_hbm_frac": round(_gbs(nbytes, dec_ms) / HBM_PEAK_GBS, 4),
+            "decode_us_per_step": round(dec_ms * 1e3 / steps, 2),
+            "decode_us_per_layer_launch": round(dec_ms * 1e3 / steps / L, 2),
+            "note": "P = 513..768 keys: each launch reads ~1.5 MB, so decode is "
+                    "launch-latency-bound, not HBM-bound"}
+
+
+def _fill(torch, tlkv, lib, sh, layer, kd, n, gen, ring=0):
+    """Append n seeded rows (positions 0..n-1; a ring layer keeps the last
+    `ring`) in chunks of at most 4096 rows."""
+    CH = 4096
+    buf_k = torch.randn((CH, kd), generator=gen, device="cuda")
+    buf_v = torch.randn((CH, kd), generator=gen, device="cuda")
+    p0 = max(0, n - ring) if ring else 0
+    p = p0
+    while p < n:
+        m = min(CH, n - p)
+        tlkv.check(lib.tl_kv_append(layer.desc, tlkv.ptr(buf_k), tlkv.ptr(buf_v), kd, None,
+                                    p, m, sh))
+        p += m
+
+
+def run_config2(torch, tlkv, lib, sh, gen, steps=512):
+    """Config 2, Qwen2.5-7B KV (L28 Hq28 Hkv4 d128, gqa 7): 8 sessions, each
+    with an 8192-row cache, `steps` batched decode steps: one
+    tl_attn_decode_batch launch per layer serves all 8 sessions (fused
+    one-row append each).  RoPE NEOX theta 1e6 on the step's q/k."""
+    L, Hq, Hkv, d, n_seq, P0 = 28, 28, 4, 128, 8, 8192
+    kd, qd = Hkv * d, Hq * d
+    c = dict(Hq=Hq, Hkv=Hkv, d=d)
+    cap = P0 + steps + 8
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    stream = torch.cuda.current_stream()
+    keep = []
+    layers = [[tlkv.Layer(cap, Hkv, d) for _ in range(L)] for _ in range(n_seq)]
+    for sl in layers:
+        for lay in sl:
+            _fill(torch, tlkv, lib, sh, lay, kd, P0, gen)
+    slots = torch.arange(cap, dtype=torch.int32, device="cuda")
+    q = torch.randn((n_seq, L, qd), generator=gen, device="cuda")
+    k = torch.randn((n_seq, L, kd), generator=gen, device="cuda")
+    v = torch.randn((n_seq, L, kd), generator=gen, device="cuda")
+    out = torch.empty((n_seq, L, qd), device="cuda")
+    for i in range(n_seq):
+        tlkv.check(lib.tl_rope(tlkv.ptr(q[i]), L, qd, Hq, d, d, P0, 1e6, 1, sh))
+        tlkv.check(lib.tl_rope(tlkv.ptr(k[i]), L, kd, Hkv, d, d, P0, 1e6, 1, sh))
+    batches = []
+    for l in range(L):
+        seqs = [tlkv.DecodeSeq(layers[i][l].desc, slots.data_ptr(), P0, 0, q[i, l].data_ptr(),
+                               k[i, l].data_ptr(), v[i, l].data_ptr(), out[i, l].data_ptr())
+                for i in range(n_seq)]
+        batches.append((tlkv.DecodeSeq * n_seq)(*seqs))
+    keep.append(batches)
+
+    def step(pos):
+        for arr in batches:
+            for i in range(n_seq):
+                arr[i].pos = pos
+            rc = lib.tl_attn_decode_batch(arr, n_seq, Hq, 0, scale, sh)
+            if rc:
+                tlkv.check(rc)
+
+    for w in range(4):
+        step(P0 + w)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    nbytes = 0
+    for s in range(steps):
+        pos = P0 + 4 + s
+        step(pos)
+        nbytes += n_seq * L * decode_bytes(c, pos + 1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return {"workload": f"config 2: L28 Hq28 Hkv4 d128 (gqa 7), 8 sessions x 8192-row cache, "
+                        f"{steps} batched decode steps (one launch per layer for all 8)",
+            "GBs": round(_gbs(nbytes, ms), 1), "hbm_frac": round(_gbs(nbytes, ms) / HBM_PEAK_GBS, 4),
+            "ms_per_step": round(ms / steps, 4),
+            "tok_s": round(n_seq * steps / (ms / 1e3), 1),
+            "us_per_layer_launch": round(ms * 1e3 / steps / L, 2)}
+
+
+def run_config5(torch, tlkv, lib, sh, gen, steps=512):
+    """Config 5, Gemma-3-4B KV (L34 Hq8 Hkv4 d256): 2 sessions at 16384 keys;
+    layers with l % 6 == 5 are global (full cache, theta 1e6), the other 29
+    are local (window 1024 on a ring of 1024 + 512 - 1 rows, theta 1e4).
+    One tl_attn_decode_batch launch per layer serves both sessions."""
+    L, Hq, Hkv, d, n_seq, P0, W = 34, 8, 4, 256, 2, 16384, 1024
+    ring = W + 512 - 1
+    kd, qd = Hkv * d, Hq * d
+    c = dict(Hq=Hq, Hkv=Hkv, d=d)
+    cap = P0 + steps + 8
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    stream = torch.cuda.current_stream()
+    glob = [l % 6 == 5 for l in range(L)]
+    layers = [[tlkv.Layer(cap if glob[l] else ring, Hkv, d, ring=0 if glob[l] else ring)
+               for l in range(L)] for _ in range(n_seq)]
+    for sl in layers:
+        for l, lay in enumerate(sl):
+            _fill(torch, tlkv, lib, sh, lay, kd, P0, gen, ring=0 if glob[l] else ring)
+    q = torch.randn((n_seq, L, qd), generator=gen, device="cuda")
+    k = torch.randn((n_seq, L, kd), generator=gen, device="cuda")
+    v = torch.randn((n_seq, L, kd), generator=gen, device="cuda")
+    out = torch.empty((n_seq, L, qd), device="cuda")
+    for i in range(n_seq):
+        for l in range(L):
+            th = 1e6 if glob[l] else 1e4
+            tlkv.check(lib.tl_rope(tlkv.ptr(q[i, l]), 1, qd, Hq, d, d, P0, th, 1, sh))
+            tlkv.check(lib.tl_rope(tlkv.ptr(k[i, l]), 1, kd, Hkv, d, d, P0, th, 1, sh))
+    batches = []
+    for l in range(L):
+        seqs = [tlkv.DecodeSeq(layers[i][l].desc, None, P0, 0, q[i, l].data_ptr(),
+                               k[i, l].data_ptr(), v[i, l].data_ptr(), out[i, l].data_ptr())
+                for i in range(n_seq)]
+        batches.append(((tlkv.DecodeSeq * n_seq)(*seqs), 0 if glob[l] else W))
+
+    def step(pos):
+        for arr, win in batches:
+            for i in range(n_seq):
+                arr[i].pos = pos
+            rc = lib.tl_attn_decode_batch(arr, n_seq, Hq, win, scale, sh)
+            if rc:
+                tlkv.check(rc)
+
+    for w in range(4):
+        step(P0 + w)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    nbytes = 0
+    B = 2 * Hkv * d * 2
+    small = Hq * d * 4 * 2 + Hkv * d * 2 * (4 + 2)
+    for s in range(steps):
+        pos = P0 + 4 + s
+        step(pos)
+        nbytes += n_seq * (5 * (pos + 1) * B + 29 * W * B + L * small)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return {"workload": f"config 5: L34 Hq8 Hkv4 d256, 2 sessions at 16384 keys, 29 local "
+                        f"layers (window 1024, ring) + 5 global, {steps} decode steps",
+            "GBs": round(_gbs(nbytes, ms), 1), "hbm_frac": round(_gbs(nbytes, ms) / HBM_PEAK_GBS, 4),
+            "ms_per_step": round(ms / steps, 4),
+            "us_per_layer_launch": round(ms * 1e3 / steps / L, 2),
+            "note": "local layers read 4 MB per launch: launch-latency-bound"}
+
+
+def run_config3(torch, tlkv, lib, sh, gen):
+    """Config 3, prefix reuse on the Qwen2.5-7B KV shape (L28 Hkv4 d128): 64
+    requests = one of 8 seeded prefixes (U[256,4096] tokens, vocab 151936) +
+    a unique suffix (U[32,512]).  Two sessions (-np 2) of 9216 rows each
+    (together 4 requests' worth, 18432 rows) take requests alternately:
+    kv_prepare_from forks a prefix that only the other session holds
+    (tl_kv_copy_between), the rest is appended (K/V write-through on all
+    layers); LRU eviction happens on demand, and every 16 requests each pool
+    is trimmed to 3/4 and compacted (one tl_kv_copy launch).  Bytes: 172032
+    per appended token, 114688 per forked or compacted row."""
+    L, Hq, Hkv, d, pool, vocab = 28, 28, 4, 128, 9216, 151936
+    kd = Hkv * d
+    rng = np.random.default_rng(0x9E3779B97F4A7C15 ^ 3)
+    prefixes = [rng.integers(0, vocab, size=int(rng.integers(256, 4097))).astype(np.uint32)
+                for _ in range(8)]
+    reqs = []
+    for r in range(64):
+        suf = rng.integers(0, vocab, size=int(rng.integers(32, 513))).astype(np.uint32)
+        reqs.append(np.concatenate([prefixes[int(rng.integers(8))], suf]))
+    stream = torch.cuda.current_stream()
+    sess = [tlkv.Session(L, Hq, Hkv, d, pool, 512, stream=sh) for _ in range(2)]
+    kbuf = torch.randn((4608, kd), generator=gen, device="cuda")
+    vbuf = torch.randn((4608, kd), generator=gen, device="cuda")
+    klist, vlist = [kbuf] * L, [vbuf] * L
+    appended = forked = compacted = evicted_trim = hits = 0
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for r, toks in enumerate(reqs):
+        S, other = sess[r % 2], sess[1 - r % 2]
+        m, resume, f = S.kv_prepare_from(other, toks)
+        forked += f
+        hits += m - f
+        S.append(toks[resume:], klist, vlist, kd)
+        appended += len(toks) - resume
+        if r % 16 == 15:
+            for X in sess:
+                ev, mv = X.compact(keep=pool * 3 // 4)
+                evicted_trim += ev
+                compacted += mv
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1)
+    nbytes = appended * 172032 + (forked + compacted) * 114688
+    L_ = tlkv._kv_sigs()
+    stats = [L_.tl_kv_cache_stats(X.radix).contents for X in sess]
+    return {"workload": "config 3: L28 Hkv4 d128, 64 requests (8 shared prefixes 256..4096 + "
+                        "unique suffix 32..512, vocab 151936), 2 sessions x 9216 rows, fork from "
+                        "the other session, LRU eviction, trim+compaction every 16 requests",
+            "GBs": round(_gbs(nbytes, ms), 1), "ms": round(ms, 2), "wall_s": round(wall, 3),
+            "appended_tokens": appended, "forked_rows": forked, "compacted_rows": compacted,
+            "local_hit_tokens": hits,
+            "radix_hit_tokens": int(sum(x.hit_tokens for x in stats)),
+            "evictions": int(sum(x.evictions for x in stats)),
+            "trim_evictions": evicted_trim,
+            "note": "time includes the host prefix cache (match, append, eviction, compaction "
+                    "planning) between launches; bytes are algorithmic"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +394,8 @@ def main():
     ap.add_argument("--no-prefill-attn", action="store_true",
                     help="fill the cache with appends only (skips phase 2)")
     ap.add_argument("--ctx", type=int, default=CFG4["ctx"])
+    ap.add_argument("--configs", default="1,2,3,5",
+                    help="other BASELINE configs to measure after the north star ('' = none)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; runs on several GPUs "
@@ -297,6 +559,15 @@ def main():
         res["prefill"] = {"TFLOPs": round(tf, 2), "frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                           "ms": round(pf_ms, 2), "flops": pf_flops,
                           "kernel": "attn_prefill_kernel<128,4> (+ split merge)"}
+    del layers, slots, q, k, v, out
+    torch.cuda.empty_cache()
+    others = {}
+    runners = {"1": run_config1, "2": run_config2, "3": run_config3, "5": run_config5}
+    for cid in [x for x in args.configs.split(",") if x]:
+        others[f"config{cid}"] = runners[cid](torch, tlkv, lib, sh, gen)
+        torch.cuda.empty_cache()
+    if others:
+        res["other_configs"] = others
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(c, c["ctx"] + 1, args.cpu_layers)
     print(json.dumps(res), flush=True)

@@ -113,6 +113,29 @@ u64  tl_kv_cache_clock(const KvRadixCache *c);
  * and reset; lets a device mirror of req.slots upload only what changed. */
 u32  tl_kv_cache_take_dirty(KvRadixCache *c);
 
+/* ---- compaction and lookup (no reference counterpart: the reference never
+ *      moves a cached row, src/kvcache.c:59-120) ---- */
+
+/* Renumber cached slots so the n_live in-tree slots occupy [0, n_live).
+ * Writes the moves to src[i] -> dst[i] (host arrays of at least `max`
+ * entries; dst rows are always free, below every src row) and updates slot
+ * metadata, the prefix index, req.slots (marked dirty from 0), snapshots and
+ * the free stack (lowest free slot pops first).  The caller copies the rows
+ * on the device (tl_kv_copy) before any kernel reads the new slot numbers.
+ * Returns the move count, or UINT32_MAX if more than `max` are needed (then
+ * nothing changed).  Hits, evictions and the LRU order are unaffected. */
+u32  tl_kv_cache_compact(KvRadixCache *c, u32 *src, u32 *dst, u32 max);
+
+/* Evict unreferenced leaves in LRU order — the victims and order of the
+ * reference's on-demand eviction (src/kvcache.c:70-104) — until at most
+ * `keep` slots are live.  Returns the number evicted (counted in
+ * stats.evictions); stops early when nothing is evictable. */
+u32  tl_kv_cache_trim(KvRadixCache *c, u32 keep);
+
+/* Longest cached prefix of tokens[0..n) and its slots (slots may be NULL),
+ * read-only: no reference counts, LRU touches or statistics change. */
+u32  tl_kv_cache_lookup(const KvRadixCache *c, const u32 *tokens, u32 n, u32 *slots);
+
 #ifdef __cplusplus
 }
 #endif

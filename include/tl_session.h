@@ -60,6 +60,33 @@ int  tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens
                         const float *const *v, float *const *out,
                         uint32_t q_stride, uint32_t kv_stride);
 
+/* tl_session_execute without the attention: the chunk loop's
+ * kv_cache_append + slot upload + K/V write-through (the part of OP_ATTN at
+ * src/backend/cpu/cpu_op.c:995-1008) for every layer.  For callers that fill
+ * or extend a cache whose attention outputs they do not need. */
+int  tl_session_append(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
+                       const float *const *k, const float *const *v, uint32_t kv_stride);
+
+/* Prefix fork (no reference counterpart: there a prefix cached by another
+ * -np slot's Session is recomputed, src/server.c:1464-1478).  Runs
+ * tl_session_kv_prepare's match on `s`; when `donor` caches a longer prefix
+ * of tokens[0..n), rows for the difference are allocated in `s`
+ * (kv_cache_append) and copied from the donor's pool on the device
+ * (tl_kv_copy_between, on s's stream: the donor's rows must be complete in
+ * that stream's order).  *matched counts both; *forked = rows copied.  The
+ * resume rule is the same as tl_session_kv_prepare's. */
+int  tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t *tokens,
+                                uint32_t n, uint32_t *matched, uint32_t *resume,
+                                uint32_t *forked);
+
+/* Eviction compaction (no reference counterpart): evict LRU leaves until at
+ * most `keep` rows are live (tl_kv_cache_trim; UINT32_MAX = no eviction),
+ * then renumber the pool so the live rows occupy slots [0, n_live)
+ * (tl_kv_cache_compact) and move their K/V rows on the device, all layers in
+ * one launch.  Rows [n_live, ctx_size) are then free as one block.
+ * *evicted / *moved (may be NULL) = rows evicted / moved. */
+int  tl_session_compact(tl_session *s, uint32_t keep, uint32_t *evicted, uint32_t *moved);
+
 /* accessors */
 uint32_t           tl_session_pos(const tl_session *s);        /* Session.n_tokens */
 void               tl_session_set_pos(tl_session *s, uint32_t pos);

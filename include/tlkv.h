@@ -125,6 +125,15 @@ int tl_kv_copy(const tl_kv_layer *layers, uint32_t n_layer,
                const uint32_t *src, const uint32_t *dst, uint32_t n,
                void *stream);
 
+/* The same across two pools of equal row shape (capacities may differ): row
+ * src[i] of src_layers[l] -> row dst[i] of dst_layers[l].  Used to fork a
+ * cached prefix from one session into another (the reference's -np slots are
+ * separate Sessions with separate caches, src/server.c:1464-1478, and a hit
+ * in another slot's cache is recomputed there). */
+int tl_kv_copy_between(const tl_kv_layer *dst_layers, const tl_kv_layer *src_layers,
+                       uint32_t n_layer, const uint32_t *src, const uint32_t *dst,
+                       uint32_t n, void *stream);
+
 /* OP_ATTN: append the batch rows, then attend.  Decode-sized batches use the
  * split-K LDS kernel, larger ones the MFMA chunked-prefill kernel. */
 int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream);

@@ -158,7 +158,7 @@ def _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots, seed, ring=0):
     Cf32 = O.Cache(cap, n_kv, hd, f16=False)
     if pos:
         if ring:
-            for p in range(pos):
+            for p in range(max(0, pos - ring), pos):   # older rows are overwritten
                 tlkv.check(tlkv.lib().tl_kv_append(
                     L.desc, tlkv.ptr(dev(T, hist_k[p:p + 1])),
                     tlkv.ptr(dev(T, hist_v[p:p + 1])), kd, None, p, 1, None))
@@ -207,6 +207,28 @@ def test_attn_vs_oracle(T, case):
     e32 = np.abs(out - o32).max()
     assert e16 < TOL, f"vs f16-cache oracle {e16}"
     assert e32 < TOL, f"vs f32-cache (reference) oracle {e32}"
+
+
+FULL_SIZE_CASES = [
+    # BASELINE shapes at their full key counts (one layer, one decode row)
+    # n_head, n_kv, hd, cap, pos, window, permuted slots, ring
+    (32, 8, 64, 800, 767, 0, True, 0),            # config 1, last decode step
+    (28, 4, 128, 8800, 8703, 0, True, 0),         # config 2/3, last decode step
+    (32, 8, 128, 33800, 33791, 0, False, 0),      # config 4, last decode step
+    (8, 4, 256, 17000, 16895, 0, False, 0),       # config 5 global layer
+    (8, 4, 256, 1535, 16895, 1024, False, 1535),  # config 5 local layer on its ring
+]
+
+
+@pytest.mark.parametrize("case", FULL_SIZE_CASES)
+def test_attn_full_size_vs_oracle(T, case):
+    n_head, n_kv, hd, cap, pos, window, perm, ring = case
+    rng = np.random.default_rng(pos)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, 1, window, slots,
+                                    seed=pos + 1, ring=ring)
+    assert np.abs(out - o16).max() < TOL
+    assert np.abs(out - o32).max() < TOL
 
 
 def test_attn_noncontiguous_equals_contiguous(T):

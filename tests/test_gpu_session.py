@@ -35,15 +35,23 @@ def prefix_rows(tokens, p, width, salt):
 
 
 def run_session(T, n_layer, nh, nkv, hd, ctx, ub, prompts, decode_steps, window=None,
-                ring=None, seed=0):
+                ring=None, seed=0, S=None, prepare=None, between=None):
+    """Serve `prompts` in order (prefill, then `decode_steps` one-token steps),
+    checking every output against the oracle and the slot-mapped rows bit for
+    bit.  prepare(S, tokens) replaces kv_prepare; between(S, i) runs after
+    request i."""
     import tlkv
-    S = tlkv.Session(n_layer, nh, nkv, hd, ctx, ub, window=window, ring=ring)
+    if S is None:
+        S = tlkv.Session(n_layer, nh, nkv, hd, ctx, ub, window=window, ring=ring)
     rng = np.random.default_rng(seed)
     qd, kd = nh * hd, nkv * hd
     results = []
     for pi, prompt in enumerate(prompts):
         full = list(prompt) + [int(x) for x in rng.integers(0, 1000, size=decode_steps)]
-        matched, resume = S.kv_prepare(np.array(prompt, np.uint32))
+        if prepare is None:
+            matched, resume = S.kv_prepare(np.array(prompt, np.uint32))
+        else:
+            matched, resume = prepare(S, np.array(prompt, np.uint32))
         calls = [(resume, len(prompt))] + [(p, p + 1) for p in range(len(prompt), len(full))]
         outs = []
         for (a, b) in calls:
@@ -86,6 +94,8 @@ def run_session(T, n_layer, nh, nkv, hd, ctx, ub, prompts, decode_steps, window=
                 assert np.array_equal(vo.cpu().numpy().view(np.uint16).reshape(len(full), -1),
                                       O.f16_bits(allv))
         results.append((matched, resume))
+        if between is not None:
+            between(S, pi)
     return S, results
 
 
@@ -114,3 +124,89 @@ def test_session_window_ring_layer(T):
     # layer 0 windowed on a ring of win + ub - 1 rows, layer 1 global
     run_session(T, 2, 8, 4, 256, 128, 8, prompts, decode_steps=4, window=[16, 0],
                 ring=[16 + 8 - 1, 0], seed=4)
+
+
+# ---- eviction compaction and prefix fork -------------------------------------
+
+def _cached_rows(T, S, n_layer, ctx):
+    """token path -> (K rows, V rows) of every layer, for every in-tree slot."""
+    import tlkv
+    L = tlkv._kv_sigs()
+    r = S.radix
+    metas = [L.tl_kv_cache_meta(r, s).contents for s in range(ctx)]
+    live = [s for s in range(ctx) if metas[s].in_tree]
+    paths = {}
+    for s in live:
+        path, cur = [], s
+        while cur != 0xFFFFFFFF:
+            path.append(metas[cur].token)
+            cur = metas[cur].parent
+        paths[s] = tuple(reversed(path))
+    sl = T.tensor(live, dtype=T.int32, device="cuda")
+    out = {}
+    per_layer = []
+    for l in range(n_layer):
+        lay = S.layer(l)
+        ko = T.zeros((len(live), lay.n_kv_head, lay.head_dim), dtype=T.float16, device="cuda")
+        vo = T.zeros_like(ko)
+        tlkv.check(tlkv.lib().tl_kv_gather(lay, tlkv.ptr(sl), len(live), tlkv.ptr(ko),
+                                           tlkv.ptr(vo), None))
+        T.cuda.synchronize()
+        per_layer.append((ko.cpu().numpy().view(np.uint16), vo.cpu().numpy().view(np.uint16)))
+    for i, s in enumerate(live):
+        out[paths[s]] = [(k[i].tobytes(), v[i].tobytes()) for (k, v) in per_layer]
+    return out, live
+
+
+def test_session_compaction_moves_rows_exactly(T):
+    """Trim + compact between requests: every surviving cached prefix keeps its
+    rows bit for bit at its new slot, the live rows end up in [0, n_live), and
+    later requests that hit relocated prefixes still match the oracle."""
+    rng = np.random.default_rng(5)
+    n_layer, ctx = 2, 96
+    shared = [list(rng.integers(0, 1000, size=n)) for n in (18, 27)]
+    prompts = [shared[i % 2] + list(rng.integers(0, 1000, size=4 + i)) for i in range(6)]
+    stats = {"moved": 0, "evicted": 0}
+
+    def between(S, i):
+        before, live0 = _cached_rows(T, S, n_layer, ctx)
+        ev, mv = S.compact(keep=len(live0) - 8 if i % 2 else 0xFFFFFFFF)
+        stats["moved"] += mv
+        stats["evicted"] += ev
+        after, live1 = _cached_rows(T, S, n_layer, ctx)
+        assert live1 == list(range(len(live1)))
+        assert len(live1) == len(live0) - ev
+        assert set(after) <= set(before)
+        for path, rows in after.items():
+            assert rows == before[path], f"request {i}: rows of a cached prefix changed"
+
+    run_session(T, n_layer, 8, 2, 128, ctx, 16, prompts, decode_steps=2, between=between)
+    assert stats["moved"] > 0 and stats["evicted"] > 0
+
+
+def test_session_fork_from_donor(T):
+    """A prefix cached by one session is copied into another (tl_kv_copy_between)
+    instead of recomputed: the copied rows are the donor's, bit for bit, and
+    the receiving session's outputs over them match the oracle."""
+    import tlkv
+    rng = np.random.default_rng(6)
+    n_layer, nh, nkv, hd, ctx, ub = 2, 8, 2, 128, 128, 16
+    base = list(rng.integers(0, 1000, size=37))
+    donor, _ = run_session(T, n_layer, nh, nkv, hd, ctx, ub, [base], decode_steps=0, seed=7)
+    S = tlkv.Session(n_layer, nh, nkv, hd, 160, ub)      # different pool size
+    forked = []
+
+    def prep(S_, toks):
+        m, r, f = S_.kv_prepare_from(donor, toks)
+        forked.append(f)
+        return m, r
+
+    prompts = [base + list(rng.integers(0, 1000, size=9)), base[:20] + [5, 6, 7]]
+    _, res = run_session(T, n_layer, nh, nkv, hd, 160, ub, prompts, decode_steps=2, seed=8,
+                         S=S, prepare=prep)
+    assert res[0] == (37, 37) and forked[0] == 37
+    assert res[1][0] == 20 and forked[1] == 0          # already held locally
+    a, _ = _cached_rows(T, donor, n_layer, ctx)
+    b, _ = _cached_rows(T, S, n_layer, 160)
+    for path, rows in a.items():
+        assert b[path] == rows

@@ -19,9 +19,11 @@ struct AppendParams {
 };
 
 struct CopyParams {
-    uint16_t *k[TL_COPY_MAX_LAYERS];
+    uint16_t *k[TL_COPY_MAX_LAYERS];          /* destination pool */
     uint16_t *v[TL_COPY_MAX_LAYERS];
-    uint32_t cap, n_kv, head_dim;
+    const uint16_t *ks[TL_COPY_MAX_LAYERS];   /* source pool (== k, v within a pool) */
+    const uint16_t *vs[TL_COPY_MAX_LAYERS];
+    uint32_t cap, src_cap, n_kv, head_dim;
 };
 
 /* One sequence of a decode launch (rows_per_seq rows at positions pos..). */

@@ -273,13 +273,16 @@ extern "C" int tl_kv_gather(const tl_kv_layer *L, const uint32_t *slots, uint32_
     return TL_OK;
 }
 
-/* grid: (blocks, layers-in-batch).  Copies one 16-byte vector per thread. */
+/* grid: (blocks, layers-in-batch).  Copies one 16-byte vector of K and of V
+ * per thread and grid-stride step. */
 __global__ __launch_bounds__(256) void kv_copy_kernel(const CopyParams p,
                                                       const u32 *src, const u32 *dst,
                                                       u32 n) {
     const u32 l = blockIdx.y;
-    u16 *kc = p.k[l];
-    u16 *vc = p.v[l];
+    u16 *kd = p.k[l];
+    u16 *vd = p.v[l];
+    const u16 *ks = p.ks[l];
+    const u16 *vs = p.vs[l];
     const u32 vpr = p.head_dim >> 3;
     const u64 total = (u64)n * p.n_kv * vpr;
     for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -289,38 +292,43 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(const CopyParams p,
         u32 h = (u32)(t % p.n_kv);
         u32 i = (u32)(t / p.n_kv);
         u32 s = src[i], d = dst[i];
-        if (s >= p.cap || d >= p.cap) continue;
-        u64 so = ((u64)h * p.cap + s) * p.head_dim + c * 8;
+        if (s >= p.src_cap || d >= p.cap) continue;
+        u64 so = ((u64)h * p.src_cap + s) * p.head_dim + c * 8;
         u64 dof = ((u64)h * p.cap + d) * p.head_dim + c * 8;
-        *(uint4 *)(kc + dof) = *(const uint4 *)(kc + so);
-        *(uint4 *)(vc + dof) = *(const uint4 *)(vc + so);
+        *(uint4 *)(kd + dof) = *(const uint4 *)(ks + so);
+        *(uint4 *)(vd + dof) = *(const uint4 *)(vs + so);
     }
 }
 
-extern "C" int tl_kv_copy(const tl_kv_layer *layers, uint32_t n_layer,
-                          const uint32_t *src, const uint32_t *dst, uint32_t n,
-                          void *stream) {
+static int copy_rows(const tl_kv_layer *dl, const tl_kv_layer *sl, uint32_t n_layer,
+                     const uint32_t *src, const uint32_t *dst, uint32_t n, void *stream) {
     if (n == 0 || n_layer == 0) return TL_OK;
-    if (!layers || !src || !dst) return tl_fail(TL_EINVAL, "copy: null pointer");
+    if (!dl || !sl || !src || !dst) return tl_fail(TL_EINVAL, "copy: null pointer");
     for (u32 l0 = 0; l0 < n_layer; l0 += TL_COPY_MAX_LAYERS) {
         u32 nl = n_layer - l0 < TL_COPY_MAX_LAYERS ? n_layer - l0 : TL_COPY_MAX_LAYERS;
         CopyParams p;
         memset(&p, 0, sizeof(p));
         for (u32 j = 0; j < nl; j++) {
-            const tl_kv_layer *L = &layers[l0 + j];
-            int rc = check_layer(L);
+            const tl_kv_layer *D = &dl[l0 + j], *S = &sl[l0 + j];
+            int rc = check_layer(D);
+            if (!rc) rc = check_layer(S);
             if (rc) return rc;
-            if (L->ring) return tl_fail(TL_EINVAL, "copy: ring layers hold no slot rows");
+            if (D->ring || S->ring) return tl_fail(TL_EINVAL, "copy: ring layers hold no slot rows");
+            if (S->n_kv_head != D->n_kv_head || S->head_dim != D->head_dim)
+                return tl_fail(TL_EINVAL, "copy: source and destination differ in shape");
             if (j == 0) {
-                p.cap = L->cap;
-                p.n_kv = L->n_kv_head;
-                p.head_dim = L->head_dim;
-            } else if (L->cap != p.cap || L->n_kv_head != p.n_kv ||
-                       L->head_dim != p.head_dim) {
+                p.cap = D->cap;
+                p.src_cap = S->cap;
+                p.n_kv = D->n_kv_head;
+                p.head_dim = D->head_dim;
+            } else if (D->cap != p.cap || S->cap != p.src_cap || D->n_kv_head != p.n_kv ||
+                       D->head_dim != p.head_dim) {
                 return tl_fail(TL_EINVAL, "copy: layers differ in shape");
             }
-            p.k[j] = (u16 *)L->k;
-            p.v[j] = (u16 *)L->v;
+            p.k[j] = (u16 *)D->k;
+            p.v[j] = (u16 *)D->v;
+            p.ks[j] = (const u16 *)S->k;
+            p.vs[j] = (const u16 *)S->v;
         }
         u64 total = (u64)n * p.n_kv * (p.head_dim >> 3);
         u64 blocks = (total + 255) / 256;
@@ -330,6 +338,18 @@ extern "C" int tl_kv_copy(const tl_kv_layer *layers, uint32_t n_layer,
         HIP_TRY(hipGetLastError());
     }
     return TL_OK;
+}
+
+extern "C" int tl_kv_copy(const tl_kv_layer *layers, uint32_t n_layer,
+                          const uint32_t *src, const uint32_t *dst, uint32_t n,
+                          void *stream) {
+    return copy_rows(layers, layers, n_layer, src, dst, n, stream);
+}
+
+extern "C" int tl_kv_copy_between(const tl_kv_layer *dst_layers, const tl_kv_layer *src_layers,
+                                  uint32_t n_layer, const uint32_t *src, const uint32_t *dst,
+                                  uint32_t n, void *stream) {
+    return copy_rows(dst_layers, src_layers, n_layer, src, dst, n, stream);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -472,6 +472,97 @@ u32 kv_cache_restore(KvRadixCache *c, u32 matched, u32 n, bool *restored) {
     return 0;
 }
 
+/* ---- compaction and read-only lookup (no reference counterpart) ---------- */
+
+/* Renumber the cached slots so that the n_live in-tree slots occupy
+ * [0, n_live).  Every live slot s >= n_live moves to a free slot below
+ * n_live, lowest to lowest; moves[i] = (src[i], dst[i]).  Slot metadata,
+ * parent links, the trie's slot values, req.slots, snapshots and the
+ * evictable-leaf heap follow the move; the free stack is rebuilt so that the
+ * lowest free slot pops first, as after kv_cache_create.  Logical behaviour
+ * (hits, evictions, the LRU order) is unchanged: eviction and matching never
+ * depend on slot numbers.  Returns the number of moves, or UINT32_MAX when
+ * more than `max` moves are needed (nothing changed then). */
+u32 tl_kv_cache_compact(KvRadixCache *c, u32 *src, u32 *dst, u32 max) {
+    if (!c) return UINT32_MAX;
+    const u32 ns = c->pool.n_slots;
+    u32 n_live = 0;
+    for (u32 i = 0; i < ns; i++) n_live += c->meta[i].in_tree;
+    u32 n_moves = 0;
+    for (u32 i = n_live; i < ns; i++) n_moves += c->meta[i].in_tree;
+    if (n_moves > max || (n_moves && (!src || !dst))) return UINT32_MAX;
+    if (n_moves == 0) goto rebuild_free;
+    {
+        u32 *remap = (u32 *)malloc((size_t)ns * sizeof(u32));
+        if (!remap) return UINT32_MAX;
+        for (u32 i = 0; i < ns; i++) remap[i] = i;
+        u32 hole = 0, k = 0;
+        for (u32 s = n_live; s < ns; s++) {
+            if (!c->meta[s].in_tree) continue;
+            while (c->meta[hole].in_tree) hole++;
+            remap[s] = hole;
+            src[k] = s;
+            dst[k] = hole;
+            k++;
+            c->meta[hole] = c->meta[s];
+            c->meta[hole].in_tree = true;   /* claims the hole for the scan */
+            KvSlotMeta *m = &c->meta[s];
+            m->in_tree = false;
+            m->ref_count = 0;
+            m->child_count = 0;
+            m->parent = KV_SLOT_NONE;
+            m->snap = KV_SLOT_NONE;
+            hole++;
+        }
+        for (u32 i = 0; i < n_live; i++)
+            if (c->meta[i].parent != KV_SLOT_NONE) c->meta[i].parent = remap[c->meta[i].parent];
+        for (u32 nd = 1; nd < c->trie.n_nodes; nd++) {
+            u32 v = c->trie.nodes[nd].value;
+            if (v) c->trie.nodes[nd].value = remap[v - 1] + 1;
+        }
+        for (u32 i = 0; i < c->req.len; i++)
+            if (c->req.slots[i] < ns) c->req.slots[i] = remap[c->req.slots[i]];
+        if (c->req.len) mark_dirty(c, 0);
+        for (u32 i = 0; i < c->cap_snaps; i++)
+            if (c->snaps[i].valid && c->snaps[i].slot < ns) c->snaps[i].slot = remap[c->snaps[i].slot];
+        free(remap);
+        heap_rebuild(c);
+    }
+rebuild_free:
+    c->pool.n_free = 0;
+    for (u32 i = ns; i-- > 0;)
+        if (!c->meta[i].in_tree) c->pool.free_stack[c->pool.n_free++] = i;
+    return n_moves;
+}
+
+/* Evict least-recently-used unreferenced leaves (the victims slot_alloc
+ * would take, in the same order) until at most `keep` slots are live.
+ * Returns the number evicted; stops early when nothing is evictable. */
+u32 tl_kv_cache_trim(KvRadixCache *c, u32 keep) {
+    if (!c) return 0;
+    u32 n = 0;
+    while (c->pool.n_slots - c->pool.n_free > keep && slot_evict_one(c)) n++;
+    return n;
+}
+
+/* Length of the longest cached prefix of tokens[0..n) and its slots, without
+ * touching reference counts, the LRU clock or statistics. */
+u32 tl_kv_cache_lookup(const KvRadixCache *c, const u32 *tokens, u32 n, u32 *slots) {
+    if (!c || !c->enabled || !tokens || n == 0) return 0;
+    if (n > c->ctx_size) n = c->ctx_size;
+    u32 node = TL_TRIE_ROOT, matched = 0;
+    for (u32 i = 0; i < n; i++) {
+        u32 nx = tl_trie_child(&c->trie, node, tokens[i]);
+        if (nx == TL_TRIE_NONE || c->trie.nodes[nx].value == 0) break;
+        u32 slot = c->trie.nodes[nx].value - 1;
+        if (slot >= c->pool.n_slots || !c->meta[slot].in_tree) break;
+        if (slots) slots[i] = slot;
+        node = nx;
+        matched = i + 1;
+    }
+    return matched;
+}
+
 /* ---- accessors ------------------------------------------------------------ */
 
 const KvRequestState *tl_kv_cache_req(const KvRadixCache *c) { return c ? &c->req : NULL; }

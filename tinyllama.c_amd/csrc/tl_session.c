@@ -23,6 +23,8 @@ struct tl_session {
     uint32_t      *tokens;      /* [ctx_size] host token history (Session.tokens) */
     uint32_t       n_tokens;    /* Session.n_tokens */
     uint32_t      *d_slots;     /* device mirror of req.slots */
+    uint32_t      *d_moves;     /* device [2 * ctx_size]: copy sources, destinations */
+    uint32_t      *h_moves;     /* host   [2 * ctx_size] */
     uint32_t      *stage;       /* pinned */
     uint32_t       stage_pos;
     float          scale;
@@ -40,6 +42,8 @@ void tl_session_destroy(tl_session *s) {
     kv_cache_destroy(s->radix);
     free(s->tokens);
     if (s->d_slots) (void)hipFree(s->d_slots);
+    if (s->d_moves) (void)hipFree(s->d_moves);
+    free(s->h_moves);
     if (s->stage) (void)hipHostFree(s->stage);
     free(s);
 }
@@ -83,7 +87,10 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
             tl_session_destroy(s);
             return fail(TL_ENOMEM, "session: kv_cache_create failed");
         }
-        if (hipMalloc((void **)&s->d_slots, (size_t)cfg->ctx_size * sizeof(uint32_t)) != hipSuccess ||
+        s->h_moves = (uint32_t *)malloc((size_t)cfg->ctx_size * 2 * sizeof(uint32_t));
+        if (!s->h_moves ||
+            hipMalloc((void **)&s->d_slots, (size_t)cfg->ctx_size * sizeof(uint32_t)) != hipSuccess ||
+            hipMalloc((void **)&s->d_moves, (size_t)cfg->ctx_size * 2 * sizeof(uint32_t)) != hipSuccess ||
             hipHostMalloc((void **)&s->stage, STAGE_WORDS * sizeof(uint32_t), 0) != hipSuccess) {
             s->stage = NULL;
             tl_session_destroy(s);
@@ -95,27 +102,45 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
     return TL_OK;
 }
 
-/* upload req.slots[lo..hi) to the device mirror, in stream order */
-static int upload_slots(tl_session *s, uint32_t lo, uint32_t hi) {
+/* copy host words to device memory in stream order through the pinned ring */
+static int upload_words(tl_session *s, uint32_t *d_dst, const uint32_t *src, uint32_t n_words) {
     hipStream_t st = (hipStream_t)s->cfg.stream;
-    const KvRequestState *req = tl_kv_cache_req(s->radix);
-    while (lo < hi) {
-        uint32_t n = hi - lo;
+    while (n_words) {
+        uint32_t n = n_words;
         if (n > STAGE_WORDS) n = STAGE_WORDS;
         if (s->stage_pos + n > STAGE_WORDS) {
             /* staged words may still be read by queued copies */
             if (hipStreamSynchronize(st) != hipSuccess) return fail(TL_EHIP, "session: sync");
             s->stage_pos = 0;
         }
-        uint32_t *dst = s->stage + s->stage_pos;
-        memcpy(dst, req->slots + lo, (size_t)n * sizeof(uint32_t));
-        if (hipMemcpyAsync(s->d_slots + lo, dst, (size_t)n * sizeof(uint32_t),
-                           hipMemcpyHostToDevice, st) != hipSuccess)
-            return fail(TL_EHIP, "session: slot upload");
+        uint32_t *stg = s->stage + s->stage_pos;
+        memcpy(stg, src, (size_t)n * sizeof(uint32_t));
+        if (hipMemcpyAsync(d_dst, stg, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice,
+                           st) != hipSuccess)
+            return fail(TL_EHIP, "session: upload");
         s->stage_pos += n;
-        lo += n;
+        d_dst += n;
+        src += n;
+        n_words -= n;
     }
     return TL_OK;
+}
+
+/* upload req.slots[lo..hi) to the device mirror */
+static int upload_slots(tl_session *s, uint32_t lo, uint32_t hi) {
+    if (hi <= lo) return TL_OK;
+    const KvRequestState *req = tl_kv_cache_req(s->radix);
+    for (uint32_t i = lo; i < hi; i++)
+        if (req->slots[i] >= s->cfg.ctx_size) return fail(TL_ERANGE, "session: slot outside the cache");
+    return upload_words(s, s->d_slots + lo, req->slots + lo, hi - lo);
+}
+
+/* upload whatever part of req.slots changed since the last upload */
+static int sync_slots(tl_session *s) {
+    uint32_t lo = tl_kv_cache_take_dirty(s->radix);
+    uint32_t len = tl_kv_cache_req(s->radix)->len;
+    if (lo == KV_SLOT_NONE || lo >= len) return TL_OK;
+    return upload_slots(s, lo, len);
 }
 
 int tl_session_kv_prepare(tl_session *s, const uint32_t *tokens, uint32_t n,
@@ -141,12 +166,11 @@ int tl_session_kv_prepare(tl_session *s, const uint32_t *tokens, uint32_t n,
     return TL_OK;
 }
 
-int tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
-                       const float *const *q, const float *const *k,
-                       const float *const *v, float *const *out,
-                       uint32_t q_stride, uint32_t kv_stride) {
-    if (!s || !tokens || n_tokens == 0) return fail(TL_EINVAL, "execute: missing tokens");
-    if (!q || !k || !v || !out) return fail(TL_EINVAL, "execute: missing activations");
+/* The chunk loop of graph_execute; q == NULL runs the K/V write-through only. */
+static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
+                      const float *const *q, const float *const *k,
+                      const float *const *v, float *const *out,
+                      uint32_t q_stride, uint32_t kv_stride) {
     const uint32_t pos = s->n_tokens;
     if ((uint64_t)pos + n_tokens > s->cfg.ctx_size)
         return fail(TL_ERANGE, "execute: batch exceeds ctx_size");
@@ -163,14 +187,17 @@ int tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
             if (req->len < p0 + chunk) return fail(TL_ERANGE, "execute: request map too short");
             uint32_t lo = tl_kv_cache_take_dirty(s->radix);
             if (lo != KV_SLOT_NONE && lo < p0 + chunk) {
-                for (uint32_t i = lo; i < p0 + chunk; i++)
-                    if (req->slots[i] >= s->cfg.ctx_size)
-                        return fail(TL_ERANGE, "execute: slot outside the cache");
                 int rc = upload_slots(s, lo, p0 + chunk);
                 if (rc) return rc;
             }
         }
-        for (uint32_t l = 0; l < s->cfg.n_layer; l++) {
+        for (uint32_t l = 0; l < s->cfg.n_layer && !q; l++) {
+            int rc = tl_kv_append(&s->layers[l], k[l] + (size_t)done * kv_stride,
+                                  v[l] + (size_t)done * kv_stride, kv_stride,
+                                  s->radix ? s->d_slots : NULL, p0, chunk, s->cfg.stream);
+            if (rc) return rc;
+        }
+        for (uint32_t l = 0; l < s->cfg.n_layer && q; l++) {
             tl_attn_args a;
             memset(&a, 0, sizeof(a));
             a.q = q[l] + (size_t)done * q_stride;
@@ -191,6 +218,91 @@ int tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
         done += chunk;
     }
     s->n_tokens = pos + n_tokens;
+    return TL_OK;
+}
+
+int tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
+                       const float *const *q, const float *const *k,
+                       const float *const *v, float *const *out,
+                       uint32_t q_stride, uint32_t kv_stride) {
+    if (!s || !tokens || n_tokens == 0) return fail(TL_EINVAL, "execute: missing tokens");
+    if (!q || !k || !v || !out) return fail(TL_EINVAL, "execute: missing activations");
+    return run_chunks(s, tokens, n_tokens, q, k, v, out, q_stride, kv_stride);
+}
+
+int tl_session_append(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
+                      const float *const *k, const float *const *v, uint32_t kv_stride) {
+    if (!s || !tokens || n_tokens == 0) return fail(TL_EINVAL, "append: missing tokens");
+    if (!k || !v) return fail(TL_EINVAL, "append: missing activations");
+    return run_chunks(s, tokens, n_tokens, NULL, k, v, NULL, 0, kv_stride);
+}
+
+/* Compaction: optional LRU trim, then renumber the pool so live rows occupy
+ * [0, n_live), moving the rows on the device in one copy launch. */
+int tl_session_compact(tl_session *s, uint32_t keep, uint32_t *evicted, uint32_t *moved) {
+    if (moved) *moved = 0;
+    if (evicted) *evicted = 0;
+    if (!s) return fail(TL_EINVAL, "compact: no session");
+    if (!s->radix) return TL_OK;
+    uint32_t ev = tl_kv_cache_trim(s->radix, keep);
+    if (evicted) *evicted = ev;
+    const uint32_t ctx = s->cfg.ctx_size;
+    uint32_t *src = s->h_moves, *dst = s->h_moves + ctx;
+    uint32_t n = tl_kv_cache_compact(s->radix, src, dst, ctx);
+    if (n == UINT32_MAX) return fail(TL_ERANGE, "compact: move list overflow");
+    if (n) {
+        int rc = upload_words(s, s->d_moves, src, n);
+        if (!rc) rc = upload_words(s, s->d_moves + ctx, dst, n);
+        if (!rc) rc = tl_kv_copy(s->layers, s->cfg.n_layer, s->d_moves, s->d_moves + ctx, n,
+                                 s->cfg.stream);
+        if (!rc) rc = sync_slots(s);
+        if (rc) return rc;
+    }
+    if (moved) *moved = n;
+    return TL_OK;
+}
+
+/* Prefix fork: like tl_session_kv_prepare, but a longer prefix cached in
+ * `donor` is first copied into this session's pool (rows allocated through
+ * kv_cache_append, copied on the device), so it need not be recomputed. */
+int tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t *tokens,
+                               uint32_t n, uint32_t *matched, uint32_t *resume,
+                               uint32_t *forked) {
+    if (forked) *forked = 0;
+    if (!donor || donor == s || !s || !s->radix || !donor->radix)
+        return tl_session_kv_prepare(s, tokens, n, matched, resume);
+    if (matched) *matched = 0;
+    if (resume) *resume = 0;
+    if (!tokens || n == 0) return TL_OK;
+    if (s->has_ring || donor->has_ring) return fail(TL_EINVAL, "fork: ring layers hold no slot rows");
+    if (donor->cfg.n_layer != s->cfg.n_layer || donor->cfg.n_kv_head != s->cfg.n_kv_head ||
+        donor->cfg.head_dim != s->cfg.head_dim)
+        return fail(TL_EINVAL, "fork: sessions differ in shape");
+    const uint32_t ctx = s->cfg.ctx_size;
+    uint32_t m = kv_cache_match(s->radix, tokens, n);
+    uint32_t *src = s->h_moves, *dst = s->h_moves + ctx;
+    uint32_t lim = n < ctx ? n : ctx;
+    uint32_t md = tl_kv_cache_lookup(donor->radix, tokens, lim, src);
+    if (md > m) {
+        const uint32_t nc = md - m;
+        if (!kv_cache_append(s->radix, tokens, m, nc)) return fail(TL_ERANGE, "fork: KV slot allocation failed");
+        const KvRequestState *req = tl_kv_cache_req(s->radix);
+        if (req->len < md) return fail(TL_ERANGE, "fork: request map too short");
+        memcpy(dst, req->slots + m, (size_t)nc * sizeof(uint32_t));
+        int rc = upload_words(s, s->d_moves, src + m, nc);
+        if (!rc) rc = upload_words(s, s->d_moves + ctx, dst, nc);
+        if (!rc) rc = tl_kv_copy_between(s->layers, donor->layers, s->cfg.n_layer, s->d_moves,
+                                         s->d_moves + ctx, nc, s->cfg.stream);
+        if (!rc) rc = sync_slots(s);
+        if (rc) return rc;
+        if (forked) *forked = nc;
+        m = md;
+    }
+    uint32_t r = m == 0 ? 0 : (m < n ? m : m - 1);
+    s->n_tokens = r;
+    if (r) memcpy(s->tokens, tokens, (size_t)r * sizeof(uint32_t));
+    if (matched) *matched = m;
+    if (resume) *resume = r;
     return TL_OK;
 }
 

@@ -57,6 +57,8 @@ def lib():
         "tl_kv_append": [ctypes.POINTER(KvLayer), vp, vp, u32, vp, u32, u32, vp],
         "tl_kv_gather": [ctypes.POINTER(KvLayer), vp, u32, vp, vp, vp],
         "tl_kv_copy": [ctypes.POINTER(KvLayer), u32, vp, vp, u32, vp],
+        "tl_kv_copy_between": [ctypes.POINTER(KvLayer), ctypes.POINTER(KvLayer), u32, vp, vp,
+                               u32, vp],
         "tl_attn": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_noappend": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_decode_batch": [ctypes.POINTER(DecodeSeq), u32, u32, u32,
@@ -163,6 +165,12 @@ def _kv_sigs():
     L.tl_kv_cache_clock.restype = ctypes.c_uint64
     L.tl_kv_cache_take_dirty.argtypes = [vp]
     L.tl_kv_cache_take_dirty.restype = u32
+    L.tl_kv_cache_compact.argtypes = [vp, u32p, u32p, u32]
+    L.tl_kv_cache_compact.restype = u32
+    L.tl_kv_cache_lookup.argtypes = [vp, u32p, u32, u32p]
+    L.tl_kv_cache_lookup.restype = u32
+    L.tl_kv_cache_trim.argtypes = [vp, u32]
+    L.tl_kv_cache_trim.restype = u32
     _kv_sigs_done = True
     return L
 
@@ -225,6 +233,30 @@ class KvCache:
     def take_dirty(self):
         return int(self.L.tl_kv_cache_take_dirty(self.h))
 
+    def compact(self, max_moves=None):
+        """Renumber live slots into [0, n_live); returns (src, dst) move arrays."""
+        import numpy as np
+        m = self.ctx if max_moves is None else max_moves
+        src = np.zeros(max(m, 1), dtype=np.uint32)
+        dst = np.zeros(max(m, 1), dtype=np.uint32)
+        n = self.L.tl_kv_cache_compact(self.h, src.ctypes.data_as(ctypes.POINTER(u32)),
+                                       dst.ctypes.data_as(ctypes.POINTER(u32)), m)
+        if n == 0xFFFFFFFF:
+            raise TlError("compaction needs more moves than allowed")
+        return src[:n].copy(), dst[:n].copy()
+
+    def trim(self, keep):
+        """Evict LRU leaves until at most `keep` slots are live; returns evictions."""
+        return int(self.L.tl_kv_cache_trim(self.h, keep))
+
+    def lookup(self, tokens):
+        """Read-only longest cached prefix: (length, slots)."""
+        import numpy as np
+        a, p = _u32_array(tokens)
+        out = np.zeros(max(a.size, 1), dtype=np.uint32)
+        n = self.L.tl_kv_cache_lookup(self.h, p, a.size, out.ctypes.data_as(ctypes.POINTER(u32)))
+        return int(n), out[:n].copy()
+
 
 # ---- session (include/tl_session.h) -------------------------------------------
 
@@ -259,6 +291,15 @@ class Session:
             L.tl_session_radix.restype = vp
             L.tl_session_layer.argtypes = [vp, u32]
             L.tl_session_layer.restype = ctypes.POINTER(KvLayer)
+            L.tl_session_kv_prepare_from.argtypes = [vp, vp, ctypes.POINTER(u32), u32,
+                                                     ctypes.POINTER(u32), ctypes.POINTER(u32),
+                                                     ctypes.POINTER(u32)]
+            L.tl_session_kv_prepare_from.restype = ctypes.c_int
+            L.tl_session_compact.argtypes = [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
+            L.tl_session_compact.restype = ctypes.c_int
+            L.tl_session_append.argtypes = [vp, ctypes.POINTER(u32), u32, ctypes.POINTER(vp),
+                                            ctypes.POINTER(vp), u32]
+            L.tl_session_append.restype = ctypes.c_int
             L._sess_sigs = True
         self.L = L
         self.n_layer = n_layer
@@ -283,6 +324,30 @@ class Session:
         m, r = u32(), u32()
         check(self.L.tl_session_kv_prepare(self.h, p, a.size, ctypes.byref(m), ctypes.byref(r)))
         return int(m.value), int(r.value)
+
+    def kv_prepare_from(self, donor, tokens):
+        """Match, forking a longer prefix from `donor`: (matched, resume, forked)."""
+        a, p = _u32_array(tokens)
+        m, r, f = u32(), u32(), u32()
+        check(self.L.tl_session_kv_prepare_from(self.h, donor.h, p, a.size, ctypes.byref(m),
+                                                ctypes.byref(r), ctypes.byref(f)))
+        return int(m.value), int(r.value), int(f.value)
+
+    def compact(self, keep=0xFFFFFFFF):
+        """Trim to `keep` live rows (LRU), then compact: (evicted, moved)."""
+        e, n = u32(), u32()
+        check(self.L.tl_session_compact(self.h, keep, ctypes.byref(e), ctypes.byref(n)))
+        return int(e.value), int(n.value)
+
+    @property
+    def radix(self):
+        return self.L.tl_session_radix(self.h)
+
+    def append(self, tokens, k, v, kv_stride):
+        """K/V write-through only (per-layer device tensors [n_tokens][kv_stride])."""
+        a, p = _u32_array(tokens)
+        arr = lambda ts: (vp * self.n_layer)(*[t.data_ptr() for t in ts])
+        check(self.L.tl_session_append(self.h, p, a.size, arr(k), arr(v), kv_stride))
 
     def execute(self, tokens, q, k, v, out, q_stride, kv_stride):
         """q/k/v/out: per-layer device tensors [n_tokens][stride]."""
