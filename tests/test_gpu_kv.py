@@ -296,6 +296,28 @@ def test_split_count_invariance(T):
     assert np.abs(outs[0] - outs[2]).max() < 1e-4
 
 
+@pytest.mark.parametrize("shape", [(32, 8, 128, 8192, 8000), (28, 4, 128, 3000, 2900),
+                                   (32, 8, 64, 1024, 700), (8, 4, 256, 4096, 4000)])
+def test_decode_variants_agree(T, shape):
+    """In-launch split merge (last workgroup of a group) vs the separate merge
+    kernel, and the 4 KB (default) vs 8 KB wave tiles: same result up to
+    rounding, and each within tolerance of the oracle."""
+    n_head, n_kv, hd, cap, pos = shape
+    outs = []
+    for env in ({}, {"TL_DECODE_MERGE_KERNEL": "1"}, {"TL_DECODE_TILE": "8192"},
+                {"TL_DECODE_TILE": "8192", "TL_DECODE_MERGE_KERNEL": "1"}):
+        os.environ.update(env)
+        try:
+            out, o16, _, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, 1, 0, None, seed=pos)
+        finally:
+            for k in env:
+                del os.environ[k]
+        assert np.abs(out - o16).max() < TOL, env
+        outs.append(out)
+    for o in outs[1:]:
+        assert np.abs(outs[0] - o).max() < 1e-4
+
+
 def test_decode_batch_sessions(T):
     """Multi-session one-token decode equals per-session OP_ATTN."""
     import tlkv

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #define TL_DEV __device__ __forceinline__
+#define TL_HOSTDEV __host__ __device__ __forceinline__
 
 typedef uint16_t u16;
 typedef uint32_t u32;

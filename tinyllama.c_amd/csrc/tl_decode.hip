@@ -8,23 +8,27 @@
  * out = softmax(s) @ V.
  *
  * Work decomposition (gfx950, wave64):
- *   grid = (n_split, n_kv_head, rows).  A workgroup (4 waves) streams one
- *   contiguous range of at most TL_DEC_MAX_CHUNK keys of one kv-head and
+ *   grid = n_split x (rows x n_kv_head) workgroups of 4 waves, two resident
+ *   per CU, mapped so that all splits of one (row, kv-head) group run on one
+ *   XCD.  A workgroup streams one contiguous chunk of keys of one kv-head and
  *   serves every q-head of the GQA group from the same K/V bytes, so each
- *   cache byte is read from HBM once per step instead of gqa times.
- *   The chunk's slot indices are staged in LDS first, so K/V loads never wait
- *   on a dependent slot-table load.
- *   A key row (D f16) is read by LPR = D/8 lanes, 16 bytes each (one
- *   global_load_dwordx4), so a wave load instruction covers KPW = 64/LPR whole
- *   rows.  Loads are double-buffered in registers: batch b+1 is in flight
- *   while batch b is computed.
+ *   cache byte is read from HBM once per step instead of gqa times.  The
+ *   chunk's slot indices are staged in LDS first, so K/V loads never wait on
+ *   a dependent slot-table load.
+ *   Each wave owns every 4th tile of the chunk (4 KB of K+V by default):
+ *   16-byte loads into registers, written to a per-wave LDS tile (K chunks
+ *   XOR-swizzled by row against bank conflicts) while the next tile's loads
+ *   are in flight.
  *   Scores: v_dot2_f32_f16 of the f16 K row with q (pre-scaled by
- *   scale*log2(e), rounded to f16), summed over the LPR lanes with DPP row
- *   moves.  Each lane group keeps its own online-softmax state per q-head
- *   (running max m, sum l, acc[8 dims]) in f32; PV uses v_fma_mix_f32 on the
- *   f16 V elements.  States merge across lane groups with shuffles, across
- *   waves through LDS, and across splits in the last workgroup to finish
- *   (atomic counter; the counter is reset by that workgroup).
+ *   scale*log2(e), rounded to f16), summed over the row's lanes with DPP
+ *   moves; wave-uniform online softmax per q-head in f32 with exp2; p is
+ *   rounded to f16 and PV runs as v_dot2 over key pairs of V.
+ *   States merge across waves through LDS and across splits in the last
+ *   workgroup of the group to finish (partials written with device-coherent
+ *   stores, a per-group atomic counter that this workgroup resets), or in a
+ *   separate merge launch when the partials exceed that workgroup's LDS.
+ *   The fused append of decode rows: the split-0 workgroup writes the new
+ *   K/V rows; workgroups that need a new key convert it from the f32 input.
  */
 #include "tl_common.h"
 #include "tl_internal.h"
@@ -55,14 +59,14 @@ TL_DEV uint4 ld_stream(const u16 *ptr) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int D>
+template <int D, int TB>
 struct DCfg {
     static constexpr int CPR = D / 8;           /* 16-byte chunks per row */
-    static constexpr int TK = 4096 / D;         /* keys per wave tile */
+    static constexpr int TK = TB / (2 * D);     /* keys per wave tile */
     static constexpr int LPK = D / 32;          /* lanes per key in QK (4 chunks each) */
     static constexpr int CPL = 4;               /* chunks per lane in QK */
     static constexpr int KPP = 64 / LPK;        /* keys per QK pass */
-    static constexpr int PASSES = TK / KPP;     /* = 2 */
+    static constexpr int PASSES = TK / KPP;     /* 1 or 2 */
     static constexpr int UNITS = TK * CPR;      /* 512 units per tile */
     static constexpr int LD = UNITS / 64;       /* 16-byte loads per lane per tile */
     static constexpr int DPL = (D <= 128) ? 2 : 4;  /* PV dims per lane */
@@ -74,9 +78,27 @@ struct DCfg {
 TL_DEV u32 perm_lo(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 TL_DEV u32 perm_hi(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
+/* the buffer builtins take and return GCC vectors; read their elements with
+ * v[i] into scalars (this compiler mis-reads __builtin_bit_cast of a vector
+ * element) */
+typedef u32 u32x4v_t __attribute__((vector_size(16)));
+typedef u32 u32x2v_t __attribute__((vector_size(8)));
+
+/* Raw buffer resource over `base` (offsets are bytes from base). */
+TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7ffffff0, 0x00020000);
+}
+/* Cache policy sc1: device-coherent access (written through to / read from
+ * the level every XCD sees), the policy of agent-scope atomics. */
+#define TL_SC1 16
+
 template <int D, int G>
+TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
+                        float *s_hl);
+
+template <int D, int G, int TB>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
-    using C = DCfg<D>;
+    using C = DCfg<D, TB>;
     constexpr int CPR = C::CPR, TK = C::TK, LPK = C::LPK, CPL = C::CPL, KPP = C::KPP;
     constexpr int PASSES = C::PASSES, UNITS = C::UNITS, LD = C::LD, DPL = C::DPL;
     constexpr int PVL = C::PVL, KG = C::KG, NPAIR = C::NPAIR;
@@ -376,6 +398,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
 
     /* ---- merge the 4 waves; write the final row or this split's partial ---- */
     const bool single = (n_split == 1);
+    const bool last_merges = p.counters != nullptr;
     for (int o = tid; o < G * D; o += 256) {
         const int h = o / D, d = o % D;
         float mm = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
@@ -390,11 +413,120 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
         const u32 hq = kvh * G + h;
         if (single) {
             sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] = O / L;
+        } else if (last_merges) {
+            /* device-coherent stores: the merging workgroup may run on
+             * another XCD and reads them with device-coherent loads */
+            const u32 pb = ((grow * p.n_head + kvh * G) * n_split) ;
+            const u32 pi = (u32)h * n_split + split;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O),
+                                                  buf_rsrc(p.ws_acc + (u64)pb * D),
+                                                  (pi * D + d) * 4, 0, TL_SC1);
+            if (d == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
+                    buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
         } else {
             u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
             p.ws_acc[pi * D + d] = O;
             if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
         }
+    }
+    if (single || !last_merges) return;
+
+    /* ---- the last split of this (row, kv-head) group to finish merges ----
+     * Its partial stores are complete (vmcnt 0) before the counter add, so
+     * the workgroup that sees n_split - 1 reads every partial. */
+    __shared__ u32 s_last;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&p.counters[grp], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_last != n_split - 1) return;
+    if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    split_merge<D, G>(p, grow, kvh, si, r, (float *)&s_kv[0][0][0], &s_l[0][0]);
+}
+
+/* Merge of the n_split partials of one (row, kv-head) group inside the
+ * decode launch: weights w_s = exp2(m_s - M) per head, O = sum w_s acc_s,
+ * out = O / sum w_s l_s.  lds: >= 2*G*n_split + 4*256 floats. */
+template <int D, int G>
+TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
+                        float *s_hl) {
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const u32 ns = p.n_split;
+    const u32 pb = (grow * p.n_head + kvh * G) * ns;
+    const __amdgpu_buffer_rsrc_t rml = buf_rsrc(p.ws_ml + pb);
+    const __amdgpu_buffer_rsrc_t racc = buf_rsrc(p.ws_acc + (u64)pb * D);
+    float *s_w = lds;                 /* [G][ns] max, then weight */
+    float *s_lv = lds + G * ns;       /* [G][ns] sums */
+    float4 *s_part = (float4 *)(lds + 2 * G * ns + ((2 * G * ns) & 3 ? 4 - ((2 * G * ns) & 3) : 0));
+    for (u32 i = tid; i < G * ns; i += 256) {
+        const u32x2v_t ml = __builtin_amdgcn_raw_buffer_load_b64(rml, i * 8, 0, TL_SC1);
+        s_w[i] = __uint_as_float(ml[0]);
+        s_lv[i] = __uint_as_float(ml[1]);
+    }
+    __syncthreads();
+    for (int h = wave; h < G; h += 4) {
+        float mx = NEG_INF;
+        for (u32 s = lane; s < ns; s += 64) mx = fmaxf(mx, s_w[h * ns + s]);
+        mx = group_max<64>(mx);
+        const float mu = (mx == NEG_INF) ? 0.f : mx;
+        float L = 0.f;
+        for (u32 s = lane; s < ns; s += 64) {
+            const float w = fast_exp2(s_w[h * ns + s] - mu);
+            s_w[h * ns + s] = w;
+            L += w * s_lv[h * ns + s];
+        }
+        L = group_sum<64>(L);
+        if (lane == 0) s_hl[h] = L;
+    }
+    __syncthreads();
+    constexpr int COLS = G * D / 4;                       /* float4 columns */
+    constexpr int SUBS = COLS >= 256 ? 1 : 256 / COLS;    /* thread subsets over splits */
+    constexpr int B = 8;
+    for (int it = tid; it < COLS * SUBS; it += 256) {
+        const int col = it % COLS, sub = it / COLS;
+        const int h = col / (D / 4);
+        const u32 cb = (u32)h * ns * D + (u32)(col % (D / 4)) * 4;   /* floats, split 0 */
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (u32 s0 = sub; s0 < ns; s0 += SUBS * B) {
+            u32x4v_t v[B];
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const u32 s = s0 + b * SUBS;
+                v[b] = s < ns ? __builtin_amdgcn_raw_buffer_load_b128(racc, (cb + s * D) * 4, 0, TL_SC1)
+                              : u32x4v_t{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const u32 s = s0 + b * SUBS;
+                const float w = s < ns ? s_w[h * ns + s] : 0.f;
+                acc.x = fmaf(w, __uint_as_float(v[b][0]), acc.x);
+                acc.y = fmaf(w, __uint_as_float(v[b][1]), acc.y);
+                acc.z = fmaf(w, __uint_as_float(v[b][2]), acc.z);
+                acc.w = fmaf(w, __uint_as_float(v[b][3]), acc.w);
+            }
+        }
+        s_part[sub * COLS + col] = acc;
+    }
+    __syncthreads();
+    const DecSeq &sq = p.seq[si];
+    for (int col = tid; col < COLS; col += 256) {
+        float4 o = s_part[col];
+        for (int sb = 1; sb < SUBS; sb++) {
+            const float4 t = s_part[sb * COLS + col];
+            o.x += t.x; o.y += t.y; o.z += t.z; o.w += t.w;
+        }
+        const int h = col / (D / 4), d = (col % (D / 4)) * 4;
+        const float inv = 1.0f / s_hl[h];
+        float *dst = sq.dst + (u64)r * p.q_stride + (u64)(kvh * G + h) * D + d;
+        dst[0] = o.x * inv;
+        dst[1] = o.y * inv;
+        dst[2] = o.z * inv;
+        dst[3] = o.w * inv;
     }
 }
 
@@ -479,21 +611,33 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p) {
     }
 }
 
+/* One decode kernel instance: entry point and K+V bytes per wave tile.
+ * The default is 4 KB (16 keys at head_dim 128): small tiles give each wave
+ * more pipeline iterations per chunk and keep GQA groups of up to 8 heads
+ * within two waves per SIMD.  8 KB tiles remain selectable
+ * (TL_DECODE_TILE=8192) for groups of up to 4 heads. */
+struct DecKernel {
+    const void *fn;
+    int tile_bytes;
+};
+
 template <int D>
-static int launch_decode_d(const DecParams &p, int G, dim3 grid, hipStream_t st) {
+static DecKernel pick_kernel(int G, int tb) {
     switch (G) {
-#define TL_CASE(g)                                                                 \
-    case g:                                                                        \
-        hipLaunchKernelGGL((attn_decode_kernel<D, g>), grid, dim3(256), 0, st, p); \
-        break;
-        TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
+#define TL_CASE(g)                                                                        \
+    case g:                                                                               \
+        return {(const void *)attn_decode_kernel<D, g, 4096>, 4096};
+#define TL_CASE8(g)                                                                       \
+    case g:                                                                               \
+        if (tb == 8192) return {(const void *)attn_decode_kernel<D, g, 8192>, 8192};      \
+        return {(const void *)attn_decode_kernel<D, g, 4096>, 4096};
+        TL_CASE8(1) TL_CASE8(2) TL_CASE8(3) TL_CASE8(4)
         TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
 #undef TL_CASE
+#undef TL_CASE8
     default:
-        return tl_fail(TL_EINVAL, "gqa ratio %d unsupported (1..8)", G);
+        return {nullptr, 0};
     }
-    HIP_TRY(hipGetLastError());
-    return TL_OK;
 }
 
 static u32 env_u32(const char *name, u32 dflt) {
@@ -502,7 +646,6 @@ static u32 env_u32(const char *name, u32 dflt) {
     return (u32)strtoul(s, NULL, 10);
 }
 
-/* Pick the split count and launch.  max_vis = most visible keys of any row. */
 static int cu_count() {
     static int cus[16] = {0};
     int dev = 0;
@@ -516,13 +659,44 @@ static int cu_count() {
     return cus[dev];
 }
 
-/* Pick the split count and launch.  max_vis = most visible keys of any row.
- * The grid is sized to 2 workgroups per CU (the LDS of one workgroup allows
- * two resident per CU), so every CU gets the same number of equal chunks. */
+/* resident workgroups per CU of a kernel (cached per entry point) */
+static int resident_per_cu(const void *fn) {
+    static const void *keys[64];
+    static int vals[64];
+    static int n = 0;
+    for (int i = 0; i < n; i++)
+        if (keys[i] == fn) return vals[i];
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, 256, 0) != hipSuccess || b < 1) b = 1;
+    if (n < 64) {
+        keys[n] = fn;
+        vals[n++] = b;
+    }
+    return b;
+}
+
+/* Pick the kernel, the split count and launch.  max_vis = most visible keys
+ * of any row.  The grid is one full wave of resident workgroups (every CU
+ * gets the same number of equal key chunks).  The partials of a split group
+ * are merged by the group's last workgroup when they fit its LDS, else by
+ * attn_merge_kernel. */
 int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
                      u32 max_vis, hipStream_t st) {
-    const u32 tk = 4096 / head_dim;           /* keys per wave tile */
-    const u32 target = env_u32("TL_DECODE_WGS", 2 * (u32)cu_count());
+    const int tb_env = (int)env_u32("TL_DECODE_TILE", 0);
+    DecKernel K;
+    switch (head_dim) {
+    case 64: K = pick_kernel<64>((int)G, tb_env); break;
+    case 128: K = pick_kernel<128>((int)G, tb_env); break;
+    case 256: K = pick_kernel<256>((int)G, tb_env); break;
+    default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
+    }
+    if (!K.fn) return tl_fail(TL_EINVAL, "gqa ratio %u unsupported (1..8)", G);
+    const u32 tk = (u32)K.tile_bytes / (2 * head_dim);   /* keys per wave tile */
+    /* two workgroups per CU: measured best on MI355X for both tile sizes
+     * (one resident wave of workgroups; more per CU only shortens chunks) */
+    int per_cu = resident_per_cu(K.fn);
+    if (per_cu > 2) per_cu = 2;
+    const u32 target = env_u32("TL_DECODE_WGS", (u32)(per_cu * cu_count()));
     const u64 n_groups = (u64)n_rows_total * p.n_kv;
     u32 n_split = (u32)((target + n_groups - 1) / n_groups);
     const u32 max_split = (max_vis + 4 * tk - 1) / (4 * tk);    /* >= one tile per wave */
@@ -536,24 +710,21 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
         return tl_fail(TL_EINVAL, "decode: %u keys need %u splits", max_vis, n_split);
     p.chunk = chunk;
     p.n_split = n_split;
+    p.counters = nullptr;
+    const bool in_kernel_merge = n_split > 1 && G * n_split <= 2048 &&
+                                 !env_u32("TL_DECODE_MERGE_KERNEL", 0);
     if (n_split > 1) {
         TlWorkspace *w;
         size_t parts = (size_t)n_rows_total * p.n_head * n_split;
-        int rc = tl_workspace_get(parts * head_dim, parts, 0, &w);
+        int rc = tl_workspace_get(parts * head_dim, parts, in_kernel_merge ? n_groups : 0, &w);
         if (rc) return rc;
         p.ws_acc = w->acc;
         p.ws_ml = (float2 *)w->ml;
+        if (in_kernel_merge) p.counters = w->cnt;
     }
-
-    dim3 grid(n_split * p.n_kv * n_rows_total);
-    int rc;
-    switch (head_dim) {
-    case 64: rc = launch_decode_d<64>(p, (int)G, grid, st); break;
-    case 128: rc = launch_decode_d<128>(p, (int)G, grid, st); break;
-    case 256: rc = launch_decode_d<256>(p, (int)G, grid, st); break;
-    default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
-    }
-    if (rc || n_split == 1) return rc;
+    void *args[] = {(void *)&p};
+    HIP_TRY(hipLaunchKernel(K.fn, dim3(n_split * (u32)n_groups), dim3(256), args, 0, st));
+    if (n_split == 1 || in_kernel_merge) return TL_OK;
     return tl_launch_merge(p, n_rows_total, head_dim, st);
 }
 

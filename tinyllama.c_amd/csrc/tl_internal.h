@@ -43,6 +43,8 @@ struct DecParams {
     uint32_t chunk, n_split;
     float *ws_acc;           /* split partials: [rows][n_head][n_split][D] */
     float2 *ws_ml;           /* split (max, sum): [rows][n_head][n_split] */
+    uint32_t *counters;      /* [rows * n_kv] finished splits per group; NULL =
+                                partials are merged by attn_merge_kernel */
 };
 
 /* Chunked-prefill launch (one OP_ATTN batch of one session). */

@@ -37,7 +37,7 @@ struct KvRadixCache {
     Session        *s;
     u32             ctx_size;
     bool            enabled;
-    u32            *path;        /* [ctx_size] eviction key scratch */
+    u32            *node_of;     /* [ctx_size] trie node holding each in-tree slot */
     /* cursor: trie node of the prefix cur_key[0..cur_len) */
     u32            *cur_key;     /* [ctx_size] */
     u32             cur_len;
@@ -184,18 +184,11 @@ static void slot_free(KvRadixCache *c, u32 slot) {
 static bool slot_evict_one(KvRadixCache *c) {
     u32 victim = heap_take(c);
     if (victim == KV_SLOT_NONE) return false;
-    /* the victim's key is the token chain up to the root */
-    u32 depth = 0;
-    for (u32 cur = victim; cur != KV_SLOT_NONE; cur = c->meta[cur].parent) {
-        if (depth >= c->ctx_size) return false;
-        c->path[depth++] = c->meta[cur].token;
-    }
-    for (u32 i = 0; i < depth / 2; i++) {
-        u32 t = c->path[i];
-        c->path[i] = c->path[depth - 1 - i];
-        c->path[depth - 1 - i] = t;
-    }
-    tl_trie_remove(&c->trie, c->path, depth);
+    /* the reference rebuilds the victim's key from the parent chain and
+     * removes it (src/kvcache.c:82-96); the trie node holding the victim is
+     * known, so the same key is removed without re-walking it */
+    tl_trie_remove_node(&c->trie, c->node_of[victim]);
+    c->node_of[victim] = TL_TRIE_NONE;
     u32 parent = c->meta[victim].parent;
     slot_free(c, victim);
     if (parent != KV_SLOT_NONE && c->meta[parent].child_count > 0) {
@@ -229,7 +222,7 @@ void kv_cache_destroy(KvRadixCache *c) {
     free(c->pool.free_stack);
     free(c->meta);
     free(c->req.slots);
-    free(c->path);
+    free(c->node_of);
     free(c->cur_key);
     free(c->heap);
     if (c->snaps) {
@@ -251,11 +244,11 @@ KvRadixCache *kv_cache_create(Session *s, KvCache *kv, u32 ctx_size) {
     c->pool.free_stack = (u32 *)malloc((size_t)ctx_size * sizeof(u32));
     c->meta = (KvSlotMeta *)calloc(ctx_size, sizeof(KvSlotMeta));
     c->req.slots = (u32 *)malloc((size_t)ctx_size * sizeof(u32));
-    c->path = (u32 *)malloc((size_t)ctx_size * sizeof(u32));
+    c->node_of = (u32 *)malloc((size_t)ctx_size * sizeof(u32));
     c->cur_key = (u32 *)malloc((size_t)ctx_size * sizeof(u32));
     c->heap_cap = 4 * ctx_size + 16;
     c->heap = (HeapEnt *)malloc((size_t)c->heap_cap * sizeof(HeapEnt));
-    if (!c->pool.free_stack || !c->meta || !c->req.slots || !c->path || !c->cur_key ||
+    if (!c->pool.free_stack || !c->meta || !c->req.slots || !c->node_of || !c->cur_key ||
         !c->heap || !tl_trie_init(&c->trie, ctx_size)) {
         kv_cache_destroy(c);
         return NULL;
@@ -267,6 +260,7 @@ KvRadixCache *kv_cache_create(Session *s, KvCache *kv, u32 ctx_size) {
         c->meta[i].parent = KV_SLOT_NONE;
         c->meta[i].snap = KV_SLOT_NONE;
         c->req.slots[i] = KV_SLOT_NONE;
+        c->node_of[i] = TL_TRIE_NONE;
     }
     c->dirty_lo = 0;
     return c;
@@ -414,6 +408,7 @@ bool kv_cache_append(KvRadixCache *c, const u32 *tokens, u32 pos, u32 n) {
             return false;
         }
         c->trie.nodes[nx].value = slot + 1;
+        c->node_of[slot] = nx;
         c->meta[slot].in_tree = true;
         c->req.len = i + 1;
         node = nx;
@@ -519,6 +514,10 @@ u32 tl_kv_cache_compact(KvRadixCache *c, u32 *src, u32 *dst, u32 max) {
         for (u32 nd = 1; nd < c->trie.n_nodes; nd++) {
             u32 v = c->trie.nodes[nd].value;
             if (v) c->trie.nodes[nd].value = remap[v - 1] + 1;
+        }
+        for (u32 k2 = 0; k2 < k; k2++) {
+            c->node_of[dst[k2]] = c->node_of[src[k2]];
+            c->node_of[src[k2]] = TL_TRIE_NONE;
         }
         for (u32 i = 0; i < c->req.len; i++)
             if (c->req.slots[i] < ns) c->req.slots[i] = remap[c->req.slots[i]];

@@ -157,8 +157,11 @@ uint32_t tl_trie_walk(const TlTrie *t, uint32_t from, const uint32_t *key, uint3
 }
 
 void tl_trie_remove(TlTrie *t, const uint32_t *key, uint32_t len) {
-    uint32_t n = tl_trie_walk(t, TL_TRIE_ROOT, key, len);
-    if (n == TL_TRIE_NONE || n == TL_TRIE_ROOT || t->nodes[n].value == 0) return;
+    tl_trie_remove_node(t, tl_trie_walk(t, TL_TRIE_ROOT, key, len));
+}
+
+void tl_trie_remove_node(TlTrie *t, uint32_t n) {
+    if (n == TL_TRIE_NONE || n == TL_TRIE_ROOT || n >= t->n_nodes || t->nodes[n].value == 0) return;
     t->nodes[n].value = 0;
     /* prune: a node with no value and no children leads to no key */
     while (n != TL_TRIE_ROOT && t->nodes[n].value == 0 && t->nodes[n].n_child == 0) {

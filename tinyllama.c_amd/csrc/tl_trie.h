@@ -53,6 +53,9 @@ uint32_t tl_trie_walk(const TlTrie *t, uint32_t from, const uint32_t *key, uint3
 /* clear the value stored at key[0..len) and free nodes that no longer lead
  * to any key; no-op when the key is absent */
 void     tl_trie_remove(TlTrie *t, const uint32_t *key, uint32_t len);
+/* the same for the key that ends at node `n` (a node id returned by
+ * tl_trie_child / tl_trie_child_make whose value is set) */
+void     tl_trie_remove_node(TlTrie *t, uint32_t n);
 /* number of keys currently stored (nodes with a value) */
 uint32_t tl_trie_count(const TlTrie *t);
 
