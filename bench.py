@@ -17,7 +17,8 @@ Inputs are seeded N(0,1) f32 (torch generator on the device) with RoPE NORM
 (theta 5e5) applied to Q and K before they are handed over.
 
 One JSON line is printed; besides the contract fields:
-  roofline      the decode attention launch (decode kernel + split merge):
+  roofline      the decode attention launch (one kernel; its key splits are
+                merged by the last workgroup of each group inside the launch):
                 algorithmic bytes per launch / average launch time, measured
                 with HIP events on the launch stream on every 8th step
   cpu_baseline  the reference's own op_attn (oracle/_ref, compiled from the
@@ -90,7 +91,7 @@ def cpu_baseline(c, P, n_layers_sample):
 
 
 def profiled_traffic():
-    """HBM bytes per decode launch pair from the committed rocprofv3 FETCH_SIZE /
+    """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (profiles/attn_decode_llama3-8b-32k_hbm_traffic.md)."""
     path = os.path.join(ROOT, "profiles", "attn_decode_llama3-8b-32k_hbm_traffic.md")
     try:
@@ -551,8 +552,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(),
-                     "kernel": "attn_decode_kernel<128,4> + attn_merge_kernel<128> "
-                               "(one OP_ATTN launch pair)"},
+                     "kernel": "attn_decode_kernel<128,4,4096> (one OP_ATTN launch, "
+                               "split merge inside)"},
     }
     if not args.no_prefill_attn:
         tf = pf_flops / (pf_ms / 1e3) / 1e12

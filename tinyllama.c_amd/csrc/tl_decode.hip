@@ -450,11 +450,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
 
 /* Merge of the n_split partials of one (row, kv-head) group inside the
  * decode launch: weights w_s = exp2(m_s - M) per head, O = sum w_s acc_s,
- * out = O / sum w_s l_s.  lds: >= 2*G*n_split + 4*256 floats. */
+ * out = O / sum w_s l_s.  Up to 32 partial float4 per thread and all (m, l)
+ * pairs are requested together, so the common case costs one round trip
+ * to memory; larger merges stream in batches.  lds: >= 2*G*n_split + 4*256
+ * floats. */
 template <int D, int G>
 TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
                         float *s_hl) {
     constexpr float NEG_INF = -__builtin_huge_valf();
+    constexpr int COLS = G * D / 4;                       /* float4 columns */
+    constexpr int SUBS = COLS >= 256 ? 1 : 256 / COLS;    /* thread subsets over splits */
+    constexpr int NIT = (COLS * SUBS + 255) / 256;        /* columns per thread */
+    constexpr int BIG = 32 / NIT;    /* partials per column when all fit in one request wave */
+    constexpr int B = 8 / NIT;       /* partials per column per batch otherwise */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const u32 ns = p.n_split;
     const u32 pb = (grow * p.n_head + kvh * G) * ns;
@@ -463,54 +471,84 @@ TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, fl
     float *s_w = lds;                 /* [G][ns] max, then weight */
     float *s_lv = lds + G * ns;       /* [G][ns] sums */
     float4 *s_part = (float4 *)(lds + 2 * G * ns + ((2 * G * ns) & 3 ? 4 - ((2 * G * ns) & 3) : 0));
+
+    /* thread column k: it = tid + 256 k -> head h, dims (col % (D/4)) * 4,
+     * splits sub, sub + SUBS, ... */
+#define TL_COL(k)                                                                     \
+    const int it = tid + (k) * 256;                                                   \
+    const int col = it % COLS, sub = it / COLS;                                       \
+    const bool live = it < COLS * SUBS;                                               \
+    const u32 cb = (u32)(col / (D / 4)) * ns * D + (u32)(col % (D / 4)) * 4;          \
+    const int h = col / (D / 4);                                                      \
+    (void)h; (void)cb; (void)live
+#define TL_LOAD(dst, s) \
+    dst = (live && (s) < ns) ? __builtin_amdgcn_raw_buffer_load_b128(racc, (cb + (s) * D) * 4, 0, TL_SC1) \
+                             : u32x4v_t{0u, 0u, 0u, 0u}
+#define TL_FMA(a, v, s)                                                               \
+    do {                                                                              \
+        const float w_ = (live && (s) < ns) ? s_w[h * ns + (s)] : 0.f;                \
+        a.x = fmaf(w_, __uint_as_float(v[0]), a.x);                                   \
+        a.y = fmaf(w_, __uint_as_float(v[1]), a.y);                                   \
+        a.z = fmaf(w_, __uint_as_float(v[2]), a.z);                                   \
+        a.w = fmaf(w_, __uint_as_float(v[3]), a.w);                                   \
+    } while (0)
+
+    const bool one_wave = ns <= (u32)(SUBS * BIG);
+    u32x4v_t v[NIT][BIG];
+    if (one_wave) {
+#pragma unroll
+        for (int k = 0; k < NIT; k++) {
+            TL_COL(k);
+#pragma unroll
+            for (int b = 0; b < BIG; b++) TL_LOAD(v[k][b], sub + b * SUBS);
+        }
+    }
     for (u32 i = tid; i < G * ns; i += 256) {
         const u32x2v_t ml = __builtin_amdgcn_raw_buffer_load_b64(rml, i * 8, 0, TL_SC1);
         s_w[i] = __uint_as_float(ml[0]);
         s_lv[i] = __uint_as_float(ml[1]);
     }
     __syncthreads();
-    for (int h = wave; h < G; h += 4) {
+    for (int hh = wave; hh < G; hh += 4) {
         float mx = NEG_INF;
-        for (u32 s = lane; s < ns; s += 64) mx = fmaxf(mx, s_w[h * ns + s]);
+        for (u32 s = lane; s < ns; s += 64) mx = fmaxf(mx, s_w[hh * ns + s]);
         mx = group_max<64>(mx);
         const float mu = (mx == NEG_INF) ? 0.f : mx;
         float L = 0.f;
         for (u32 s = lane; s < ns; s += 64) {
-            const float w = fast_exp2(s_w[h * ns + s] - mu);
-            s_w[h * ns + s] = w;
-            L += w * s_lv[h * ns + s];
+            const float w = fast_exp2(s_w[hh * ns + s] - mu);
+            s_w[hh * ns + s] = w;
+            L += w * s_lv[hh * ns + s];
         }
         L = group_sum<64>(L);
-        if (lane == 0) s_hl[h] = L;
+        if (lane == 0) s_hl[hh] = L;
     }
     __syncthreads();
-    constexpr int COLS = G * D / 4;                       /* float4 columns */
-    constexpr int SUBS = COLS >= 256 ? 1 : 256 / COLS;    /* thread subsets over splits */
-    constexpr int B = 8;
-    for (int it = tid; it < COLS * SUBS; it += 256) {
-        const int col = it % COLS, sub = it / COLS;
-        const int h = col / (D / 4);
-        const u32 cb = (u32)h * ns * D + (u32)(col % (D / 4)) * 4;   /* floats, split 0 */
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (u32 s0 = sub; s0 < ns; s0 += SUBS * B) {
-            u32x4v_t v[B];
+    float4 acc[NIT];
 #pragma unroll
-            for (int b = 0; b < B; b++) {
-                const u32 s = s0 + b * SUBS;
-                v[b] = s < ns ? __builtin_amdgcn_raw_buffer_load_b128(racc, (cb + s * D) * 4, 0, TL_SC1)
-                              : u32x4v_t{0u, 0u, 0u, 0u};
-            }
+    for (int k = 0; k < NIT; k++) {
+        acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        TL_COL(k);
+        if (one_wave) {
 #pragma unroll
-            for (int b = 0; b < B; b++) {
-                const u32 s = s0 + b * SUBS;
-                const float w = s < ns ? s_w[h * ns + s] : 0.f;
-                acc.x = fmaf(w, __uint_as_float(v[b][0]), acc.x);
-                acc.y = fmaf(w, __uint_as_float(v[b][1]), acc.y);
-                acc.z = fmaf(w, __uint_as_float(v[b][2]), acc.z);
-                acc.w = fmaf(w, __uint_as_float(v[b][3]), acc.w);
+            for (int b = 0; b < BIG; b++) TL_FMA(acc[k], v[k][b], sub + b * SUBS);
+        } else {
+            for (u32 s0 = sub; s0 < ns; s0 += B * SUBS) {
+                u32x4v_t t[B];
+#pragma unroll
+                for (int b = 0; b < B; b++) TL_LOAD(t[b], s0 + b * SUBS);
+#pragma unroll
+                for (int b = 0; b < B; b++) TL_FMA(acc[k], t[b], s0 + b * SUBS);
             }
         }
-        s_part[sub * COLS + col] = acc;
+    }
+#undef TL_COL
+#undef TL_LOAD
+#undef TL_FMA
+#pragma unroll
+    for (int k = 0; k < NIT; k++) {
+        const int it = tid + k * 256;
+        if (it < COLS * SUBS) s_part[(it / COLS) * COLS + it % COLS] = acc[k];
     }
     __syncthreads();
     const DecSeq &sq = p.seq[si];
