@@ -19,8 +19,9 @@ Inputs are seeded N(0,1) f32 (torch generator on the device) with RoPE NORM
 One JSON line is printed; besides the contract fields:
   roofline      the decode attention launch (one kernel; its key splits are
                 merged by the last workgroup of each group inside the launch):
-                algorithmic bytes per launch / average launch time, measured
-                with HIP events on the launch stream on every 8th step
+                algorithmic bytes per launch / average launch time, the timed
+                region's HIP-event time on the launch stream over its K x 32
+                back-to-back launches
   cpu_baseline  the reference's own op_attn (oracle/_ref, compiled from the
                 reference sources) timed on a bounded sample of the same
                 decode step, single thread
@@ -478,17 +479,13 @@ def main():
     descs = [layers[l].desc for l in range(L)]
     attn = lib.tl_attn
 
-    def step(pos, evs=None):
+    def step(pos):
         for l in range(L):
             a = args_l[l]
             a.pos = pos
-            if evs is not None:
-                evs[0][l].record(stream)
             rc = attn(descs[l], a, sh)
             if rc:
                 tlkv.check(rc)
-            if evs is not None:
-                evs[1][l].record(stream)
 
     pos = c["ctx"]
     for _ in range(args.warmup):
@@ -497,28 +494,20 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    SAMPLE = 8
-    sampled = {s: [[ev() for _ in range(L)], [ev() for _ in range(L)]]
-               for s in range(0, K, SAMPLE)}
     t_start, t_end = ev(), ev()
     pos0 = pos
     torch.cuda.synchronize()
     t_start.record(stream)
     for s in range(K):
-        step(pos, sampled.get(s))
+        step(pos)
         pos += 1
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-
-    launch_ms, launch_bytes, n_launch = 0.0, 0.0, 0
-    for s, (ea, eb) in sampled.items():
-        for l in range(L):
-            launch_ms += ea[l].elapsed_time(eb[l])
-            launch_bytes += decode_bytes(c, pos0 + s + 1)
-            n_launch += 1
-    avg_launch_us = launch_ms * 1e3 / n_launch
-    achieved = launch_bytes / n_launch / (avg_launch_us * 1e-6) / 1e9
+    # one OP_ATTN launch per layer and step, back to back on `stream`
+    avg_launch_us = total_ms * 1e3 / (K * L)
+    launch_bytes = sum(decode_bytes(c, pos0 + s + 1) for s in range(K)) / K
+    achieved = launch_bytes / (avg_launch_us * 1e-6) / 1e9
     bytes_total = sum(L * decode_bytes(c, pos0 + s + 1) for s in range(K))
     value = bytes_total / (total_ms / 1e3) / 1e9
 
