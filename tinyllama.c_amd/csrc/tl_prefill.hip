@@ -10,23 +10,30 @@
  *   A workgroup owns one kv-head, a block of 32*QB query rows and one split
  *   of the key range; its W = G*QB waves each own one q-head of the GQA group
  *   and 32 query rows, so every K/V tile staged in LDS serves G*QB*32 rows.
- *   Per 32-key tile:
- *     S^T[key][row] = K . Q^T      v_mfma_f32_32x32x16_f16, A = K rows from
- *                                  LDS, B = Q (registers, f16, pre-scaled by
- *                                  scale*log2 e); each lane ends up owning one
- *                                  query row and 16 of the tile's keys, so the
- *                                  row max / sum need one shuffle between the
- *                                  two half-waves.
- *     online softmax in f32 (exp2), P^T packed to f16 straight from the
- *                                  accumulator registers.
- *     O^T[d][row] += V^T . P^T     v_mfma_f32_32x32x16_f16, A = V^T from LDS
- *                                  (the tile is stored transposed), B = P^T.
- *                                  The MFMA's reduction index k is mapped to
- *                                  the keys each lane already holds, so P^T
- *                                  never goes through LDS.
- *   The next tile's K/V rows are loaded into registers while the current one
- *   is computed.  Key splits (when the grid would not fill the chip) write
- *   partial (O, max, sum) rows that attn_merge_kernel combines.
+ *   Per tile of BN keys (64 at head_dim <= 128, 32 at 256):
+ *     S^T[key][row] = K . Q^T      v_mfma_f32_32x32x16_f16 per 32-key block,
+ *                                  A = K rows from LDS, B = Q (registers, f16,
+ *                                  pre-scaled by scale*log2 e); each lane ends
+ *                                  up owning one query row and 16 keys of the
+ *                                  block, so the row max / sum need one shuffle
+ *                                  between the two half-waves.
+ *     online softmax in f32 (exp2); mask arithmetic only on tiles that cross
+ *                                  the causal diagonal, the window edge or the
+ *                                  range end; the O rescale is skipped when no
+ *                                  row's max moved.  P^T is packed to f16
+ *                                  straight from the accumulator registers.
+ *     O^T[d][row] += V^T . P^T     v_mfma_f32_32x32x16_f16 per 16 keys,
+ *                                  A = V^T read from the row-major V tile with
+ *                                  ds_read_b64_tr_b16 (a 4x16 -> 16x4 transpose
+ *                                  per 16-lane group), B = P^T.  The MFMA's
+ *                                  reduction index k is mapped to the keys each
+ *                                  lane already holds, so P^T never goes
+ *                                  through LDS and V is stored as loaded.
+ *   K/V tiles are double-buffered in LDS (one barrier per tile): the next
+ *   tile's rows are loaded into registers while the current one is computed
+ *   and written to the other buffer afterwards.  Key splits (when the grid
+ *   would not fill the chip) write partial (O, max, sum) rows that
+ *   attn_merge_kernel combines.
  */
 #include "tl_common.h"
 #include "tl_internal.h"
@@ -43,30 +50,46 @@ struct PCfg {
     static constexpr int QB = (WMAX / G) > 0 ? (WMAX / G) : 1;   /* 32-row query blocks */
     static constexpr int W = G * QB;                              /* waves */
     static constexpr int ROWS = 32 * QB;                          /* query rows per WG */
+    static constexpr int BN = (D <= 128) ? 64 : 32;               /* keys per tile */
 };
 
-#define TL_PF_BN 32        /* keys per tile */
-#define TL_PF_VS 36        /* V^T row stride in halves (32 keys + pad) */
+#define TL_PF_VPAD 16      /* V row padding in halves: the transpose reads of
+                              one 16-lane group hit 4 rows x 32 B, 8 banks apart */
 
 TL_DEV half8_t h8_from_u4(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
 TL_DEV u32 pack2(float a, float b) { return pack_f16x2_fast(a, b); }
 
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+/* ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+ * (i & 3) of the 4-half vector addressed by lane 4e + (i >> 2), for e = 0..3.
+ * With lane j addressing row (j >> 2), column 4 (j & 3) of a 4 x 16 block,
+ * lane i receives column i of rows 0..3: a 4x16 -> 16x4 transpose. */
+TL_DEV uint2 ld_tr16(const _Float16 *lds_ptr) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *)(lds_ptr));
+    const u32 lo = (u32)(u16)v.x | ((u32)(u16)v.y << 16);
+    const u32 hi = (u32)(u16)v.z | ((u32)(u16)v.w << 16);
+    return make_uint2(lo, hi);
+}
+
 template <int D, int G>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * PCfg<D, G>::W))) void attn_prefill_kernel(const PrefParams p) {
     using C = PCfg<D, G>;
-    constexpr int W = C::W, ROWS = C::ROWS;
+    constexpr int W = C::W, ROWS = C::ROWS, BN = C::BN;
     constexpr int T = 64 * W;
-    constexpr int BN = TL_PF_BN, VS = TL_PF_VS;
     constexpr int CPR = D / 8;           /* 16-byte chunks per row */
     constexpr int KS = D / 16;           /* k-steps of the QK MFMA */
     constexpr int DB = D / 32;           /* 32-row d-blocks of O^T */
-    constexpr int UNITS = BN * CPR;      /* 16-byte units per tile */
+    constexpr int KB = BN / 32;          /* 32-key blocks of S^T per tile */
+    constexpr int UNITS = BN * CPR;      /* 16-byte units per K (or V) tile */
     constexpr int UPT = (UNITS + T - 1) / T;
+    constexpr int VS = D + TL_PF_VPAD;   /* V row stride (halves) */
     constexpr float NEG_INF = -__builtin_huge_valf();
 
-    __shared__ uint4 s_k[UNITS];
-    __shared__ _Float16 s_vt[D * VS];
+    __shared__ uint4 s_k[2][UNITS];                      /* K rows, chunk-swizzled */
+    __shared__ __attribute__((aligned(16))) _Float16 s_v[2][BN * VS];   /* V rows, row-major */
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5;             /* half-wave */
@@ -84,6 +107,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     const u32 my_q = qb0 + qsub * 32 + lr;           /* lane's query row */
     const bool row_ok = my_q < p.n;
     const u32 qpos = p.pos + my_q;
+    /* the wave's first and last valid query positions */
+    const u32 wq0 = p.pos + qb0 + qsub * 32;
+    const u32 wq1 = p.pos + min(qb0 + qsub * 32 + 31, p.n - 1);
 
     /* key range of the workgroup, then of this split */
     const u32 wg_last = min(p.pos + qb0 + ROWS, p.pos + p.n);
@@ -139,49 +165,69 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
             }
         }
     };
-
-    if (ks < ke) load_tile(ks);
-    for (u32 tb = ks; tb < ke; tb += BN) {
-        __syncthreads();                 /* previous tile fully consumed */
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
             const int u = tid + j * T;
             if (u < UNITS) {
                 const int row = u / CPR, c = u % CPR;
-                s_k[row * CPR + (c ^ (row % CPR))] = rk[j];
-                const u32 w[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    s_vt[(c * 8 + 2 * e) * VS + row] = __builtin_bit_cast(_Float16, (u16)(w[e] & 0xffff));
-                    s_vt[(c * 8 + 2 * e + 1) * VS + row] = __builtin_bit_cast(_Float16, (u16)(w[e] >> 16));
-                }
+                s_k[buf][row * CPR + (c ^ (row % CPR))] = rk[j];
+                *(uint4 *)&s_v[buf][row * VS + c * 8] = rv[j];
             }
         }
-        __syncthreads();
-        if (tb + BN < ke) load_tile(tb + BN);
+    };
 
-        /* S^T = K . Q^T : lane holds keys 8(r/4) + 4h + r%4 of query lr */
-        floatx16_t sacc;
+    /* transpose-read coordinates of this lane (16-lane group gi, lane i) */
+    const int gi = lane >> 4, li = lane & 15;
+    const int tr_row = li >> 2;                       /* + 4h (+8) + 16 kb4 */
+    const int tr_col = 16 * (gi & 1) + 4 * (li & 3);  /* + 32 b */
+
+    int buf = 0;
+    if (ks < ke) {
+        load_tile(ks);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (u32 tb = ks; tb < ke; tb += BN) {
+        if (tb + BN < ke) load_tile(tb + BN);
+        const uint4 *sk = s_k[buf];
+        const _Float16 *sv_t = s_v[buf];
+
+        /* S^T = K . Q^T per 32-key block: lane holds keys
+         * 32 kb + 8(r/4) + 4h + r%4 of query lr */
+        floatx16_t sacc[KB];
 #pragma unroll
-        for (int r = 0; r < 16; r++) sacc[r] = 0.f;
+        for (int kb = 0; kb < KB; kb++) {
 #pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const int c = 2 * s + h;
-            const half8_t a = h8_from_u4(s_k[lr * CPR + (c ^ (lr % CPR))]);
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[s], sacc, 0, 0, 0);
+            for (int r = 0; r < 16; r++) sacc[kb][r] = 0.f;
+            const int krow = 32 * kb + lr;
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+                const int c = 2 * s + h;
+                const half8_t a = h8_from_u4(sk[krow * CPR + (c ^ (krow % CPR))]);
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[s], sacc[kb], 0, 0, 0);
+            }
         }
 
-        /* mask + online softmax */
-        float sv[16];
+        /* mask (only tiles that cross a boundary) + online softmax */
+        const bool full = tb + BN <= ke && tb + BN - 1 <= wq0 &&
+                          (!p.window || tb + p.window > wq1);
+        float sv[KB][16];
         float mt = NEG_INF;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const u32 key = tb + 8 * (r / 4) + 4 * h + (r % 4);
-            const bool ok = row_ok && key < ke && key <= qpos &&
-                            (!p.window || key + p.window > qpos);
-            sv[r] = ok ? sacc[r] : NEG_INF;
-            mt = fmaxf(mt, sv[r]);
-        }
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float v = sacc[kb][r];
+                if (!full) {
+                    const u32 key = tb + 32 * kb + 8 * (r / 4) + 4 * h + (r % 4);
+                    const bool ok = row_ok && key < ke && key <= qpos &&
+                                    (!p.window || key + p.window > qpos);
+                    v = ok ? v : NEG_INF;
+                }
+                sv[kb][r] = v;
+                mt = fmaxf(mt, v);
+            }
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float mn = fmaxf(m, mt);
         const float mu = (mn == NEG_INF) ? 0.f : mn;
@@ -189,35 +235,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
         m = mn;
         float ps = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            sv[r] = __builtin_amdgcn_exp2f(sv[r] - mu);
-            ps += sv[r];
-        }
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                sv[kb][r] = __builtin_amdgcn_exp2f(sv[kb][r] - mu);
+                ps += sv[kb][r];
+            }
         lsum = lsum * alpha + ps;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-        for (int b = 0; b < DB; b++)
+            for (int b = 0; b < DB; b++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[b][r] *= alpha;
-
-        /* P^T operands: k = 8h + j maps to the keys this lane holds */
-        const half8_t p0 = h8_from_u4(make_uint4(pack2(sv[0], sv[1]), pack2(sv[2], sv[3]),
-                                                 pack2(sv[4], sv[5]), pack2(sv[6], sv[7])));
-        const half8_t p1 = h8_from_u4(make_uint4(pack2(sv[8], sv[9]), pack2(sv[10], sv[11]),
-                                                 pack2(sv[12], sv[13]), pack2(sv[14], sv[15])));
-
-        /* O^T += V^T . P^T */
-#pragma unroll
-        for (int b = 0; b < DB; b++) {
-            const _Float16 *vr = s_vt + (32 * b + lr) * VS;
-            const uint2 x0 = *(const uint2 *)(vr + 4 * h);
-            const uint2 x1 = *(const uint2 *)(vr + 8 + 4 * h);
-            const uint2 y0 = *(const uint2 *)(vr + 16 + 4 * h);
-            const uint2 y1 = *(const uint2 *)(vr + 24 + 4 * h);
-            const half8_t a0 = h8_from_u4(make_uint4(x0.x, x0.y, x1.x, x1.y));
-            const half8_t a1 = h8_from_u4(make_uint4(y0.x, y0.y, y1.x, y1.y));
-            o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, p0, o[b], 0, 0, 0);
-            o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, p1, o[b], 0, 0, 0);
+                for (int r = 0; r < 16; r++) o[b][r] *= alpha;
         }
+
+        /* O^T += V^T . P^T per 16-key step; the MFMA's k = 8h + j maps to
+         * keys 4h + j (j < 4) and 8 + 4h + (j - 4) of the step, the keys this
+         * lane holds; V^T comes from row-major V by transpose reads */
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const int r0 = 8 * half;
+                const half8_t pp = h8_from_u4(make_uint4(
+                    pack2(sv[kb][r0 + 0], sv[kb][r0 + 1]), pack2(sv[kb][r0 + 2], sv[kb][r0 + 3]),
+                    pack2(sv[kb][r0 + 4], sv[kb][r0 + 5]), pack2(sv[kb][r0 + 6], sv[kb][r0 + 7])));
+                const int kbase = 32 * kb + 16 * half + 4 * h + tr_row;
+#pragma unroll
+                for (int b = 0; b < DB; b++) {
+                    const _Float16 *vp = sv_t + kbase * VS + 32 * b + tr_col;
+                    const uint2 x0 = ld_tr16(vp);
+                    const uint2 x1 = ld_tr16(vp + 8 * VS);
+                    const half8_t a = h8_from_u4(make_uint4(x0.x, x0.y, x1.x, x1.y));
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pp, o[b], 0, 0, 0);
+                }
+            }
+        }
+        if (tb + BN < ke) store_tile(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
     }
     lsum += __shfl_xor(lsum, 32);
 
