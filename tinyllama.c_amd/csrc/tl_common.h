@@ -26,10 +26,13 @@ TL_DEV u32 pack_f16x2(float lo, float hi) {
     return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
 }
 
-/* RNE pack without the NaN pinning (operands of dot products). */
+/* RNE pack without the NaN pinning (operands of dot products): one
+ * v_cvt_pk_f16_f32 on gfx950. */
+typedef float tl_f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 tl_f16x2_t __attribute__((ext_vector_type(2)));
 TL_DEV u32 pack_f16x2_fast(float lo, float hi) {
-    return (u32)__builtin_bit_cast(u16, (_Float16)lo) |
-           ((u32)__builtin_bit_cast(u16, (_Float16)hi) << 16);
+    const tl_f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(u32, __builtin_convertvector(v, tl_f16x2_t));
 }
 
 TL_DEV float f16lo(u32 w) {

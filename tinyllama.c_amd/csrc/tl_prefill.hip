@@ -120,6 +120,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     chunk = (chunk + BN - 1) / BN * BN;
     const u32 ks = wg_first + split * chunk;
     const u32 ke = min(ks + chunk, wg_last);
+    /* keys this lane's row may see, inside the split's range: [klo, khi) */
+    const u32 khi = row_ok ? min(ke, qpos + 1) : 0u;
+    const u32 klo = (p.window && qpos + 1 > p.window) ? qpos + 1 - p.window : 0u;
 
     /* Q operand: lane holds Q[row lr][16s + 8h .. +8], f16, log2-scaled */
     half8_t qop[KS];
@@ -198,36 +201,41 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
         floatx16_t sacc[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) sacc[kb][r] = 0.f;
             const int krow = 32 * kb + lr;
+            const floatx16_t zero = {};
+            sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                h8_from_u4(sk[krow * CPR + (h ^ (krow % CPR))]), qop[0], zero, 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < KS; s++) {
+            for (int s = 1; s < KS; s++) {
                 const int c = 2 * s + h;
                 const half8_t a = h8_from_u4(sk[krow * CPR + (c ^ (krow % CPR))]);
                 sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[s], sacc[kb], 0, 0, 0);
             }
         }
 
-        /* mask (only tiles that cross a boundary) + online softmax */
+        /* mask (only tiles that cross a boundary; visible keys of this lane's
+         * row are [klo, khi)) + online softmax */
         const bool full = tb + BN <= ke && tb + BN - 1 <= wq0 &&
                           (!p.window || tb + p.window > wq1);
         float sv[KB][16];
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) sv[kb][r] = sacc[kb][r];
+        if (!full) {
+#pragma unroll
+            for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const u32 key = tb + 32 * kb + 8 * (r / 4) + 4 * h + (r % 4);
+                    sv[kb][r] = (key >= klo) & (key < khi) ? sv[kb][r] : NEG_INF;
+                }
+        }
         float mt = NEG_INF;
 #pragma unroll
         for (int kb = 0; kb < KB; kb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float v = sacc[kb][r];
-                if (!full) {
-                    const u32 key = tb + 32 * kb + 8 * (r / 4) + 4 * h + (r % 4);
-                    const bool ok = row_ok && key < ke && key <= qpos &&
-                                    (!p.window || key + p.window > qpos);
-                    v = ok ? v : NEG_INF;
-                }
-                sv[kb][r] = v;
-                mt = fmaxf(mt, v);
-            }
+            for (int r = 0; r < 16; r++) mt = fmaxf(mt, sv[kb][r]);
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float mn = fmaxf(m, mt);
         const float mu = (mn == NEG_INF) ? 0.f : mn;
