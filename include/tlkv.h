@@ -95,6 +95,16 @@ typedef struct tl_decode_seq {
 
 #define TL_MAX_BATCH_SEQ 16
 
+/* RoPE applied inside a fused entry point (the reference's OP_ROPE_NORM /
+ * OP_ROPE_NEOX, src/backend/cpu/cpu_op.c:632-700, on Q and K before OP_ATTN).
+ * Pair i of each head rotates by angle pos * theta^(-2i/rope_dim); NORM
+ * (neox = 0) pairs elements (2i, 2i+1), NEOX pairs (i, i + rope_dim/2). */
+typedef struct tl_rope_params {
+    uint32_t rope_dim;        /* rotated elements per head (even, <= head_dim) */
+    float    theta;           /* base */
+    int32_t  neox;
+} tl_rope_params;
+
 const char *tl_last_error(void);
 
 /* Select the device for the calling thread and set up library state. */
@@ -134,6 +144,21 @@ int tl_kv_copy_between(const tl_kv_layer *dst_layers, const tl_kv_layer *src_lay
                        uint32_t n_layer, const uint32_t *src, const uint32_t *dst,
                        uint32_t n, void *stream);
 
+/* Fused RoPE + OP_ATTN (SURVEY-listed next step "fused RoPE + append"; the
+ * reference runs OP_ROPE on Q and K, cpu_op.c:637-700, then OP_ATTN,
+ * cpu_op.c:964-1064).  Same results as tl_rope(q rows at pos..), tl_rope(k
+ * rows at pos..) then tl_attn, bit for bit, in one launch for decode batches
+ * (two for prefill batches: append+RoPE, then attention).  q and k are read,
+ * not rotated in place. */
+int tl_attn_rope(const tl_kv_layer *L, const tl_attn_args *a, const tl_rope_params *rope,
+                 void *stream);
+
+/* tl_kv_append with RoPE applied to K on the way (same bits as tl_rope then
+ * tl_kv_append; k is not modified). */
+int tl_kv_append_rope(const tl_kv_layer *L, const float *k, const float *v,
+                      uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                      uint32_t n, const tl_rope_params *rope, void *stream);
+
 /* OP_ATTN: append the batch rows, then attend.  Decode-sized batches use the
  * split-K LDS kernel, larger ones the MFMA chunked-prefill kernel. */
 int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
@@ -147,6 +172,12 @@ int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
 int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
                          uint32_t n_head, uint32_t window, float scale,
                          void *stream);
+
+/* tl_attn_decode_batch with RoPE on every session's q and new k row (each at
+ * its own position), as tl_attn_rope. */
+int tl_attn_decode_batch_rope(const tl_decode_seq *seqs, uint32_t n_seq, uint32_t n_head,
+                              uint32_t window, float scale, const tl_rope_params *rope,
+                              void *stream);
 
 /* OP_ROPE_NORM (neox = 0) / OP_ROPE_NEOX (neox = 1) in place on x
  * [rows][row_stride] f32, row p at position pos+p. */

@@ -79,3 +79,64 @@ TL_DEV float group_max(float x) {
     if constexpr (N >= 64) x = fmaxf(x, __shfl_xor(x, 32));
     return x;
 }
+
+/* ---- RoPE (reference: src/backend/cpu/cpu_op.c:637-700) -------------------
+ * Pair i of a head row rotates by angle pos * theta_i, theta_i =
+ * 1 / powf(base, 2i / rdim).  NORM pairs elements (2i, 2i+1), NEOX pairs
+ * (i, i + rdim/2).  The rotation is written with explicit fmaf so every
+ * kernel that applies it (the rope op and the fused append / attention
+ * staging) produces the same bits. */
+TL_DEV void rope_rot(float a, float b, float c, float s, float &x, float &y) {
+    x = fmaf(a, c, -(b * s));
+    y = fmaf(a, s, b * c);
+}
+TL_DEV void rope_cs(u32 i, u32 rdim, float base, u32 pos, float &c, float &s) {
+    const float th = 1.0f / powf(base, (float)(2 * i) / (float)rdim);
+    sincosf((float)pos * th, &s, &c);
+}
+/* elements e0..e0+7 of one head row (hrow = its element 0), rotated at
+ * position pos when rdim > 0 */
+TL_DEV void load8_rope(const float *hrow, u32 e0, u32 pos, u32 rdim, float base, int neox,
+                       float out[8]) {
+    const float4 a = *(const float4 *)(hrow + e0);
+    const float4 b = *(const float4 *)(hrow + e0 + 4);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    if (rdim == 0 || e0 >= rdim) return;
+    if (!neox) {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            if (e0 + j < rdim) {
+                float c, s, x, y;
+                rope_cs((e0 + j) >> 1, rdim, base, pos, c, s);
+                rope_rot(out[j], out[j + 1], c, s, x, y);
+                out[j] = x;
+                out[j + 1] = y;
+            }
+        }
+        return;
+    }
+    const u32 half = rdim >> 1;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const u32 e = e0 + j;
+        if (e < rdim) {
+            const bool lo = e < half;
+            const u32 i = lo ? e : e - half;
+            const float pa = lo ? out[j] : hrow[i];           /* element i */
+            const float pb = lo ? hrow[e + half] : out[j];    /* element i + half */
+            float c, s, x, y;
+            rope_cs(i, rdim, base, pos, c, s);
+            rope_rot(pa, pb, c, s, x, y);
+            out[j] = lo ? x : y;
+        }
+    }
+}
+
+/* 8 f32 -> 8 binary16 (RNE, NaN pinned) of one K unit, RoPE'd at pos */
+TL_DEV uint4 cvt8_rope(const float *hrow, u32 e0, u32 pos, u32 rdim, float base, int neox) {
+    float t[8];
+    load8_rope(hrow, e0, pos, rdim, base, neox, t);
+    return make_uint4(pack_f16x2(t[0], t[1]), pack_f16x2(t[2], t[3]), pack_f16x2(t[4], t[5]),
+                      pack_f16x2(t[6], t[7]));
+}

@@ -96,7 +96,7 @@ template <int D, int G>
 TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
                         float *s_hl);
 
-template <int D, int G, int TB>
+template <int D, int G, int TB, bool ROPE>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     using C = DCfg<D, TB>;
     constexpr int CPR = C::CPR, TK = C::TK, LPK = C::LPK, CPL = C::CPL, KPP = C::KPP;
@@ -111,6 +111,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     __shared__ uint4 s_q[G * D / 8];             /* q, f16, scaled to log2 units */
     __shared__ float s_m[4][G];
     __shared__ float s_l[4][G];
+    __shared__ uint4 s_newk[TL_DEC_MAX_NEW][D / 8];   /* new rows of a fused launch, f16 */
+    __shared__ uint4 s_newv[TL_DEC_MAX_NEW][D / 8];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -141,22 +143,25 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
     const u32 kbeg = start + split * p.chunk;
     const u32 kend = min(kbeg + p.chunk, n_keys);
-    /* fused append: the split-0 workgroup of row 0 writes this kv-head's new
-     * rows (positions pos..pos+n-1) to the cache; every workgroup that needs
-     * a new key converts it from the f32 input itself, so no workgroup reads
-     * a cache row that is being written in this launch. */
+    /* fused append: the launch's new rows (positions pos..pos+rows-1, K
+     * RoPE'd when p.rope is set) are converted to f16 into LDS by every
+     * workgroup that reads one of them and by the split-0 workgroup of row 0,
+     * which also writes them to the cache.  No workgroup reads a cache row
+     * that is being written in this launch, and the stream loop below never
+     * runs the conversion (or RoPE) code itself. */
+    constexpr int VPR = D / 8;
     const bool fused = sq.kin != nullptr;
-    if (fused && split == 0 && r == 0) {
-        constexpr int VPR = D / 8;
+    const bool writer = fused && split == 0 && r == 0;
+    if (fused && (writer || kend > sq.pos)) {
         for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
             const u32 row = i / VPR, c8 = i % VPR;
-            const u32 key = sq.pos + row;
-            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
-            if (ph >= sq.cap) continue;
             const u64 src = (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8;
-            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
-            *(uint4 *)((u16 *)sq.k + dst) = cvt8_f16(sq.kin + src);
-            *(uint4 *)((u16 *)sq.v + dst) = cvt8_f16(sq.vin + src);
+            if constexpr (ROPE)
+                s_newk[row][c8] = cvt8_rope(sq.kin + (src - c8 * 8), c8 * 8, sq.pos + row,
+                                            p.rope.rdim, p.rope.theta, p.rope.neox);
+            else
+                s_newk[row][c8] = cvt8_f16(sq.kin + src);
+            s_newv[row][c8] = cvt8_f16(sq.vin + src);
         }
     }
 
@@ -171,18 +176,31 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
             s_slot[i - kbeg] = s < sq.cap ? s : 0u;
         }
     }
-    /* q of the GQA group, scaled to log2 units, staged once per workgroup */
+    /* q of the GQA group (RoPE'd when p.rope is set), scaled to log2 units,
+     * staged once per workgroup */
     {
         const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
         for (int i = tid; i < G * D / 8; i += 256) {
-            const float4 a = *(const float4 *)(qb + i * 8);
-            const float4 b = *(const float4 *)(qb + i * 8 + 4);
+            float t[8];
+            load8_rope(qb + (i / (D / 8)) * D, (i % (D / 8)) * 8, sq.pos + r,
+                       ROPE ? p.rope.rdim : 0u, p.rope.theta, p.rope.neox, t);
             const float sc = p.scale_log2;
-            s_q[i] = make_uint4(pack_f16x2_fast(a.x * sc, a.y * sc), pack_f16x2_fast(a.z * sc, a.w * sc),
-                                pack_f16x2_fast(b.x * sc, b.y * sc), pack_f16x2_fast(b.z * sc, b.w * sc));
+            s_q[i] = make_uint4(pack_f16x2_fast(t[0] * sc, t[1] * sc), pack_f16x2_fast(t[2] * sc, t[3] * sc),
+                                pack_f16x2_fast(t[4] * sc, t[5] * sc), pack_f16x2_fast(t[6] * sc, t[7] * sc));
         }
     }
     __syncthreads();
+    if (writer) {
+        for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
+            const u32 row = i / VPR, c8 = i % VPR;
+            const u32 key = sq.pos + row;
+            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
+            if (ph >= sq.cap) continue;
+            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
+            *(uint4 *)((u16 *)sq.k + dst) = s_newk[row][c8];
+            *(uint4 *)((u16 *)sq.v + dst) = s_newv[row][c8];
+        }
+    }
 
     /* q chunks of this lane's QK position, scaled to log2 units, f16 pairs */
     const int qc0 = (lane % LPK) * CPL;
@@ -220,9 +238,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
                 const u32 key = min(tb_ + (u32)row, klast_);                        \
                 const int kc_ = (u % CPR) ^ (row % CPR), vc_ = u % CPR;             \
                 if (key >= sq.pos) {                                                \
-                    const u64 o_ = (u64)(key - sq.pos) * sq.kv_stride + (u64)kvh * D; \
-                    rk[j] = cvt8_f16(sq.kin + o_ + kc_ * 8);                        \
-                    rv[j] = cvt8_f16(sq.vin + o_ + vc_ * 8);                        \
+                    rk[j] = s_newk[key - sq.pos][kc_];                              \
+                    rv[j] = s_newv[key - sq.pos][vc_];                              \
                 } else {                                                            \
                     const u32 ph = TL_PHYS(key);                                    \
                     rk[j] = ld_stream(Kbase + (u64)ph * D + kc_ * 8);               \
@@ -649,30 +666,27 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p) {
     }
 }
 
-/* One decode kernel instance: entry point and K+V bytes per wave tile.
- * The default is 4 KB (16 keys at head_dim 128): small tiles give each wave
- * more pipeline iterations per chunk and keep GQA groups of up to 8 heads
- * within two waves per SIMD.  8 KB tiles remain selectable
- * (TL_DECODE_TILE=8192) for groups of up to 4 heads. */
+/* One decode kernel instance: entry point and K (or V) bytes per wave tile
+ * (the RoPE-fusing instances are separate so the plain ones carry none of
+ * its code):
+ * 4 KB (16 keys at head_dim 128).  Small tiles give each wave more pipeline
+ * iterations per chunk and keep GQA groups of up to 8 heads within two waves
+ * per SIMD (8 KB tiles measured slower: 35.1 vs 31.8 us at config 4). */
 struct DecKernel {
     const void *fn;
     int tile_bytes;
 };
 
 template <int D>
-static DecKernel pick_kernel(int G, int tb) {
+static DecKernel pick_kernel(int G, bool rope) {
     switch (G) {
 #define TL_CASE(g)                                                                        \
     case g:                                                                               \
-        return {(const void *)attn_decode_kernel<D, g, 4096>, 4096};
-#define TL_CASE8(g)                                                                       \
-    case g:                                                                               \
-        if (tb == 8192) return {(const void *)attn_decode_kernel<D, g, 8192>, 8192};      \
-        return {(const void *)attn_decode_kernel<D, g, 4096>, 4096};
-        TL_CASE8(1) TL_CASE8(2) TL_CASE8(3) TL_CASE8(4)
+        if (rope) return {(const void *)attn_decode_kernel<D, g, 4096, true>, 4096};      \
+        return {(const void *)attn_decode_kernel<D, g, 4096, false>, 4096};
+        TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
         TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
 #undef TL_CASE
-#undef TL_CASE8
     default:
         return {nullptr, 0};
     }
@@ -720,12 +734,11 @@ static int resident_per_cu(const void *fn) {
  * attn_merge_kernel. */
 int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
                      u32 max_vis, hipStream_t st) {
-    const int tb_env = (int)env_u32("TL_DECODE_TILE", 0);
     DecKernel K;
     switch (head_dim) {
-    case 64: K = pick_kernel<64>((int)G, tb_env); break;
-    case 128: K = pick_kernel<128>((int)G, tb_env); break;
-    case 256: K = pick_kernel<256>((int)G, tb_env); break;
+    case 64: K = pick_kernel<64>((int)G, p.rope.rdim != 0); break;
+    case 128: K = pick_kernel<128>((int)G, p.rope.rdim != 0); break;
+    case 256: K = pick_kernel<256>((int)G, p.rope.rdim != 0); break;
     default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
     }
     if (!K.fn) return tl_fail(TL_EINVAL, "gqa ratio %u unsupported (1..8)", G);

@@ -6,8 +6,16 @@
 
 #define TL_COPY_MAX_LAYERS 64
 #define TL_PREFILL_MIN_ROWS 16
+#define TL_DEC_MAX_NEW 16          /* new rows of one fused decode launch (< TL_PREFILL_MIN_ROWS) */
 
 /* One segment of an append launch: n rows of one layer of one session. */
+/* RoPE applied on the fly (rdim == 0: none).  Same math as rope_kernel. */
+struct RopeCfg {
+    uint32_t rdim;
+    float theta;
+    int32_t neox;
+};
+
 struct AppendSeg {
     uint16_t *kc, *vc;
     const float *k, *v;
@@ -16,6 +24,7 @@ struct AppendSeg {
 };
 struct AppendParams {
     AppendSeg seg[TL_MAX_BATCH_SEQ];
+    RopeCfg rope;            /* applied to K before the conversion */
 };
 
 struct CopyParams {
@@ -43,6 +52,7 @@ struct DecParams {
     uint32_t chunk, n_split;
     float *ws_acc;           /* split partials: [rows][n_head][n_split][D] */
     float2 *ws_ml;           /* split (max, sum): [rows][n_head][n_split] */
+    RopeCfg rope;            /* applied to q and to new K rows */
     uint32_t *counters;      /* [rows * n_kv] finished splits per group; NULL =
                                 partials are merged by attn_merge_kernel */
 };
@@ -59,6 +69,7 @@ struct PrefParams {
     uint32_t n_split;
     float *ws_acc;
     float2 *ws_ml;
+    RopeCfg rope;            /* applied to q rows */
 };
 
 struct TlWorkspace {
@@ -88,4 +99,5 @@ int tl_launch_merge(const DecParams &p, uint32_t n_rows_total, uint32_t head_dim
 
 /* MFMA chunked-prefill attention (tl_prefill.hip). */
 bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a);
-int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st);
+int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, const RopeCfg &rope,
+                      hipStream_t st);

@@ -160,8 +160,10 @@ TL_DEV uint4 cvt8(const float *src) {
     return o;
 }
 
+
 /* grid: (blocks, n_seg).  One thread per 8-element vector of one row of one
  * head; consecutive threads cover consecutive 16-byte pieces of a row. */
+template <bool ROPE>
 __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
     const AppendSeg &sg = p.seg[blockIdx.y];
     const u32 vpr = sg.head_dim >> 3;
@@ -176,7 +178,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
         if (slot >= sg.cap) continue;
         u64 src = (u64)i * sg.kv_stride + (u64)h * sg.head_dim + c * 8;
         u64 dst = ((u64)h * sg.cap + slot) * sg.head_dim + c * 8;
-        *(uint4 *)(sg.kc + dst) = cvt8(sg.k + src);
+        if constexpr (ROPE)
+            *(uint4 *)(sg.kc + dst) = cvt8_rope(sg.k + (src - c * 8), c * 8, sg.pos + i,
+                                                p.rope.rdim, p.rope.theta, p.rope.neox);
+        else
+            *(uint4 *)(sg.kc + dst) = cvt8(sg.k + src);
         *(uint4 *)(sg.vc + dst) = cvt8(sg.v + src);
     }
 }
@@ -190,8 +196,12 @@ int tl_launch_append(const AppendParams &p, u32 n_seg, hipStream_t stream) {
     if (most == 0) return TL_OK;
     u64 blocks = (most + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(kv_append_kernel, dim3((u32)blocks, n_seg), dim3(256), 0,
-                       stream, p);
+    if (p.rope.rdim)
+        hipLaunchKernelGGL(kv_append_kernel<true>, dim3((u32)blocks, n_seg), dim3(256), 0,
+                           stream, p);
+    else
+        hipLaunchKernelGGL(kv_append_kernel<false>, dim3((u32)blocks, n_seg), dim3(256), 0,
+                           stream, p);
     HIP_TRY(hipGetLastError());
     return TL_OK;
 }
@@ -227,6 +237,33 @@ extern "C" int tl_kv_append(const tl_kv_layer *L, const float *k, const float *v
     AppendParams p;
     memset(&p, 0, sizeof(p));
     rc = fill_seg(p.seg[0], L, k, v, kv_stride, slots, pos, n);
+    if (rc) return rc;
+    return tl_launch_append(p, 1, (hipStream_t)stream);
+}
+
+static int rope_cfg(const tl_kv_layer *L, const tl_rope_params *r, RopeCfg &c) {
+    c.rdim = 0;
+    c.theta = 0.f;
+    c.neox = 0;
+    if (!r) return TL_OK;
+    if (r->rope_dim > L->head_dim || (r->rope_dim & 1) || !(r->theta > 0.f))
+        return tl_fail(TL_EINVAL, "rope: dim %u theta %g", r->rope_dim, (double)r->theta);
+    c.rdim = r->rope_dim;
+    c.theta = r->theta;
+    c.neox = r->neox ? 1 : 0;
+    return TL_OK;
+}
+
+extern "C" int tl_kv_append_rope(const tl_kv_layer *L, const float *k, const float *v,
+                                 uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                                 uint32_t n, const tl_rope_params *rope, void *stream) {
+    int rc = check_layer(L);
+    if (rc) return rc;
+    if (n == 0) return TL_OK;
+    AppendParams p;
+    memset(&p, 0, sizeof(p));
+    rc = fill_seg(p.seg[0], L, k, v, kv_stride, slots, pos, n);
+    if (!rc) rc = rope_cfg(L, rope, p.rope);
     if (rc) return rc;
     return tl_launch_append(p, 1, (hipStream_t)stream);
 }
@@ -371,23 +408,12 @@ __global__ __launch_bounds__(256) void rope_kernel(float *x, u32 rows, u32 row_s
         u32 h = (u32)(t % heads);
         u32 r = (u32)(t / heads);
         float *bh = x + (u64)r * row_stride + (u64)h * hdim;
-        u32 ia, ib;
-        float th;
-        if (neox) {
-            th = 1.0f / powf(base, (float)(2 * i) / (float)rdim);
-            ia = i;
-            ib = i + pairs;
-        } else {
-            th = 1.0f / powf(base, (float)(2 * i) / (float)rdim);
-            ia = 2 * i;
-            ib = 2 * i + 1;
-        }
-        float ang = (float)(pos + r) * th;
-        float s, c;
-        sincosf(ang, &s, &c);
-        float a = bh[ia], b = bh[ib];
-        bh[ia] = a * c - b * s;
-        bh[ib] = a * s + b * c;
+        const u32 ia = neox ? i : 2 * i, ib = neox ? i + pairs : 2 * i + 1;
+        float c, s, nx, ny;
+        rope_cs(i, rdim, base, pos + r, c, s);
+        rope_rot(bh[ia], bh[ib], c, s, nx, ny);
+        bh[ia] = nx;
+        bh[ib] = ny;
     }
 }
 
@@ -436,21 +462,31 @@ static int check_args(const tl_kv_layer *L, const tl_attn_args *a) {
  * fused launch (the decode kernel writes the new rows itself); prefill-sized
  * ones append first and then run the MFMA kernel. */
 static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
-                     hipStream_t st) {
+                     const RopeCfg &rope, hipStream_t st) {
     if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(L, a)) {
         if (append) {
             AppendParams ap;
             memset(&ap, 0, sizeof(ap));
             int rc = fill_seg(ap.seg[0], L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
             if (rc) return rc;
+            ap.rope = rope;
             rc = tl_launch_append(ap, 1, st);
             if (rc) return rc;
         }
-        return tl_launch_prefill(L, a, st);
+        return tl_launch_prefill(L, a, rope, st);
     }
     DecParams p;
     memset(&p, 0, sizeof(p));
-    if (append) {
+    if (append && a->n > TL_DEC_MAX_NEW) {
+        /* more new rows than a decode launch stages: append first */
+        AppendParams ap;
+        memset(&ap, 0, sizeof(ap));
+        int rc = fill_seg(ap.seg[0], L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
+        if (rc) return rc;
+        ap.rope = rope;
+        rc = tl_launch_append(ap, 1, st);
+        if (rc) return rc;
+    } else if (append) {
         AppendSeg chk;
         int rc = fill_seg(chk, L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
         if (rc) return rc;
@@ -472,6 +508,7 @@ static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
     p.q_stride = a->q_stride;
     p.window = a->window;
     p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.rope = rope;
     u32 max_keys = a->pos + a->n;
     u32 max_vis = (a->window && max_keys > a->window) ? a->window : max_keys;
     return tl_launch_decode(p, a->n, L->head_dim, a->n_head / L->n_kv_head, max_vis, st);
@@ -481,19 +518,50 @@ extern "C" int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream
     int rc = check_args(L, a);
     if (rc) return rc;
     if (a->n == 0) return TL_OK;
-    return attn_core(L, a, true, (hipStream_t)stream);
+    RopeCfg rc0;
+    rope_cfg(L, nullptr, rc0);
+    return attn_core(L, a, true, rc0, (hipStream_t)stream);
+}
+
+extern "C" int tl_attn_rope(const tl_kv_layer *L, const tl_attn_args *a,
+                            const tl_rope_params *rope, void *stream) {
+    int rc = check_args(L, a);
+    if (rc) return rc;
+    if (a->n == 0) return TL_OK;
+    RopeCfg c;
+    rc = rope_cfg(L, rope, c);
+    if (rc) return rc;
+    return attn_core(L, a, true, c, (hipStream_t)stream);
 }
 
 extern "C" int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
     int rc = check_args(L, a);
     if (rc) return rc;
     if (a->n == 0) return TL_OK;
-    return attn_core(L, a, false, (hipStream_t)stream);
+    RopeCfg rc0;
+    rope_cfg(L, nullptr, rc0);
+    return attn_core(L, a, false, rc0, (hipStream_t)stream);
 }
+
+static int decode_batch(const tl_decode_seq *seqs, uint32_t n_seq, uint32_t n_head,
+                        uint32_t window, float scale, const tl_rope_params *rope,
+                        void *stream);
 
 extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
                                     uint32_t n_head, uint32_t window, float scale,
                                     void *stream) {
+    return decode_batch(seqs, n_seq, n_head, window, scale, nullptr, stream);
+}
+
+extern "C" int tl_attn_decode_batch_rope(const tl_decode_seq *seqs, uint32_t n_seq,
+                                         uint32_t n_head, uint32_t window, float scale,
+                                         const tl_rope_params *rope, void *stream) {
+    return decode_batch(seqs, n_seq, n_head, window, scale, rope, stream);
+}
+
+static int decode_batch(const tl_decode_seq *seqs, uint32_t n_seq, uint32_t n_head,
+                        uint32_t window, float scale, const tl_rope_params *rope,
+                        void *stream) {
     if (n_seq == 0) return TL_OK;
     if (!seqs || n_seq > TL_MAX_BATCH_SEQ)
         return tl_fail(TL_EINVAL, "decode_batch: 1..%d sessions", TL_MAX_BATCH_SEQ);
@@ -538,6 +606,8 @@ extern "C" int tl_attn_decode_batch(const tl_decode_seq *seqs, uint32_t n_seq,
     p.q_stride = n_head * L0->head_dim;
     p.window = window;
     p.scale_log2 = scale * 1.4426950408889634f;
+    int rc = rope_cfg(L0, rope, p.rope);
+    if (rc) return rc;
     return tl_launch_decode(p, n_seq, L0->head_dim, n_head / L0->n_kv_head, max_vis,
                             (hipStream_t)stream);
 }

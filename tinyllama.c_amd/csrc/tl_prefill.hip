@@ -74,7 +74,7 @@ TL_DEV uint2 ld_tr16(const _Float16 *lds_ptr) {
     return make_uint2(lo, hi);
 }
 
-template <int D, int G>
+template <int D, int G, bool ROPE>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * PCfg<D, G>::W))) void attn_prefill_kernel(const PrefParams p) {
     using C = PCfg<D, G>;
     constexpr int W = C::W, ROWS = C::ROWS, BN = C::BN;
@@ -124,17 +124,19 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     const u32 khi = row_ok ? min(ke, qpos + 1) : 0u;
     const u32 klo = (p.window && qpos + 1 > p.window) ? qpos + 1 - p.window : 0u;
 
-    /* Q operand: lane holds Q[row lr][16s + 8h .. +8], f16, log2-scaled */
+    /* Q operand: lane holds Q[row lr][16s + 8h .. +8] (RoPE'd when p.rope is
+     * set), f16, log2-scaled */
     half8_t qop[KS];
     {
         const float *qrow = p.q + (u64)(row_ok ? my_q : 0) * p.q_stride + (u64)hq * D;
 #pragma unroll
         for (int s = 0; s < KS; s++) {
-            const float4 a = *(const float4 *)(qrow + 16 * s + 8 * h);
-            const float4 b = *(const float4 *)(qrow + 16 * s + 8 * h + 4);
+            float t[8];
+            load8_rope(qrow, 16 * s + 8 * h, qpos, ROPE ? p.rope.rdim : 0u, p.rope.theta,
+                       p.rope.neox, t);
             const float sc = row_ok ? p.scale_log2 : 0.f;
-            uint4 u = make_uint4(pack2(a.x * sc, a.y * sc), pack2(a.z * sc, a.w * sc),
-                                 pack2(b.x * sc, b.y * sc), pack2(b.z * sc, b.w * sc));
+            uint4 u = make_uint4(pack2(t[0] * sc, t[1] * sc), pack2(t[2] * sc, t[3] * sc),
+                                 pack2(t[4] * sc, t[5] * sc), pack2(t[6] * sc, t[7] * sc));
             qop[s] = h8_from_u4(u);
         }
     }
@@ -315,8 +317,12 @@ bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a) {
 
 template <int D, int G>
 static void launch_pf(const PrefParams &p, u32 blocks, hipStream_t st) {
-    hipLaunchKernelGGL((attn_prefill_kernel<D, G>), dim3(blocks), dim3(64 * PCfg<D, G>::W), 0,
-                       st, p);
+    if (p.rope.rdim)
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true>), dim3(blocks),
+                           dim3(64 * PCfg<D, G>::W), 0, st, p);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false>), dim3(blocks),
+                           dim3(64 * PCfg<D, G>::W), 0, st, p);
 }
 
 template <int D>
@@ -342,7 +348,8 @@ static u32 rows_per_wg(u32 D, u32 G) {
     return 32 * qb;
 }
 
-int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t st) {
+int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, const RopeCfg &rope,
+                      hipStream_t st) {
     const u32 D = L->head_dim, G = a->n_head / L->n_kv_head;
     PrefParams p;
     memset(&p, 0, sizeof(p));
@@ -360,6 +367,7 @@ int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, hipStream_t s
     p.n_kv = L->n_kv_head;
     p.window = a->window;
     p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.rope = rope;
 
     const u32 rows = rows_per_wg(D, G);
     const u32 nqb = (a->n + rows - 1) / rows;

@@ -33,6 +33,10 @@ class DecodeSeq(ctypes.Structure):
 
 MAX_BATCH_SEQ = 16
 
+
+class RopeParams(ctypes.Structure):
+    _fields_ = [("rope_dim", u32), ("theta", ctypes.c_float), ("neox", ctypes.c_int32)]
+
 _lib = None
 
 
@@ -63,6 +67,12 @@ def lib():
         "tl_attn_noappend": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_decode_batch": [ctypes.POINTER(DecodeSeq), u32, u32, u32,
                                  ctypes.c_float, vp],
+        "tl_attn_rope": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs),
+                         ctypes.POINTER(RopeParams), vp],
+        "tl_kv_append_rope": [ctypes.POINTER(KvLayer), vp, vp, u32, vp, u32, u32,
+                              ctypes.POINTER(RopeParams), vp],
+        "tl_attn_decode_batch_rope": [ctypes.POINTER(DecodeSeq), u32, u32, u32,
+                                      ctypes.c_float, ctypes.POINTER(RopeParams), vp],
         "tl_rope": [vp, u32, u32, u32, u32, u32, u32, ctypes.c_float,
                     ctypes.c_int, vp],
         "tl_probe_read": [vp, ctypes.c_uint64, vp, u32, u32, vp],
