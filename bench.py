@@ -412,7 +412,7 @@ def main():
     tlkv.check(lib.tl_init(0))
     L, Hq, Hkv, d, ub = c["L"], c["Hq"], c["Hkv"], c["d"], c["ub"]
     kd, qd = Hkv * d, Hq * d
-    cap = c["ctx"] + args.warmup + args.steps
+    cap = c["ctx"] + args.warmup + args.steps + 72   # + the RoPE comparison steps
     scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
     stream = torch.cuda.current_stream()
     sh = tlkv.stream_handle(stream)
@@ -511,6 +511,43 @@ def main():
     bytes_total = sum(L * decode_bytes(c, pos0 + s + 1) for s in range(K))
     value = bytes_total / (total_ms / 1e3) / 1e9
 
+    # decode step with RoPE on q and the new k row (the reference's OP_ROPE x2
+    # + OP_ATTN): three launches per layer (tl_rope, tl_rope, tl_attn) vs one
+    # (tl_attn_rope), on raw (un-rotated) q/k rows; cache rows written past
+    # the timed region's positions, so they never affect `value`
+    rope_steps = min(64, K)
+    rp = tlkv.RopeParams(d, c["theta"], c["rope_neox"])
+    qs = torch.randn((L, 1, qd), generator=gen, device="cuda")
+    ks = torch.randn((L, 1, kd), generator=gen, device="cuda")
+    def step_rope(pos, fused):
+        for l in range(L):
+            a = args_l[l]
+            a.pos = pos
+            if fused:
+                a.q, a.k = qs[l].data_ptr(), ks[l].data_ptr()
+                tlkv.check(lib.tl_attn_rope(descs[l], a, rp, sh))
+            else:
+                tlkv.check(lib.tl_rope(tlkv.ptr(q[l]), 1, qd, Hq, d, d, pos, c["theta"],
+                                       c["rope_neox"], sh))
+                tlkv.check(lib.tl_rope(tlkv.ptr(k[l]), 1, kd, Hkv, d, d, pos, c["theta"],
+                                       c["rope_neox"], sh))
+                a.q, a.k = q[l].data_ptr(), k[l].data_ptr()
+                tlkv.check(attn(descs[l], a, sh))
+    rope_us = {}
+    for fused in (False, True):
+        step_rope(pos, fused)
+        torch.cuda.synchronize()
+        e0, e1 = ev(), ev()
+        e0.record(stream)
+        for s in range(rope_steps):
+            step_rope(pos + s, fused)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        rope_us["fused" if fused else "separate"] = round(
+            e0.elapsed_time(e1) * 1e3 / (rope_steps * L), 2)
+    for l in range(L):
+        args_l[l].q, args_l[l].k = q[l].data_ptr(), k[l].data_ptr()
+
     res = {
         "metric": "decode KV-attn GB/s (%HBM peak) + append tok/s, Llama-3-8B shape @32K ctx",
         "value": round(value, 2),
@@ -534,6 +571,9 @@ def main():
         "decode": {"us_per_layer_launch": round(avg_launch_us, 3),
                    "tok_s": round(K / (total_ms / 1e3), 1),
                    "frac_of_measured_ceiling": round(value / ceiling, 4)},
+        "decode_with_rope_us_per_layer": {**rope_us, "steps": rope_steps,
+                                          "note": "RoPE on q and the new k row each step: "
+                                                  "tl_rope x2 + tl_attn vs tl_attn_rope"},
         "append": {"tok_s": round(app_tok_s, 1), "GBs": round(app_bytes / (app_ms / 1e3) / 1e9, 1),
                    "note": "64 x 512-row tl_kv_append per layer; a token counts once "
                            "for all 32 layers; decode appends are fused into the decode "

@@ -144,23 +144,31 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     const u32 kbeg = start + split * p.chunk;
     const u32 kend = min(kbeg + p.chunk, n_keys);
     /* fused append: the launch's new rows (positions pos..pos+rows-1, K
-     * RoPE'd when p.rope is set) are converted to f16 into LDS by every
-     * workgroup that reads one of them and by the split-0 workgroup of row 0,
-     * which also writes them to the cache.  No workgroup reads a cache row
-     * that is being written in this launch, and the stream loop below never
-     * runs the conversion (or RoPE) code itself. */
+     * RoPE'd when ROPE) are converted to f16 into LDS by every workgroup that
+     * reads one of them and by the split-0 workgroup of row 0, which also
+     * writes them to the cache.  No workgroup reads a cache row that is being
+     * written in this launch, and the stream loop never runs the conversion
+     * (or RoPE) code itself.
+     * With ROPE, q and the new K rows are first copied to LDS as f32, rotated
+     * one pair per thread while the first tile's loads are in flight, then
+     * converted. */
     constexpr int VPR = D / 8;
     const bool fused = sq.kin != nullptr;
     const bool writer = fused && split == 0 && r == 0;
-    if (fused && (writer || kend > sq.pos)) {
+    const bool need_new = fused && (writer || kend > sq.pos);
+    float *qf = (float *)&s_kv[0][0][0];             /* ROPE: [G][D] f32 */
+    float *kf = qf + G * D;                          /* ROPE: [rows][D] f32 */
+    const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
+    if (need_new) {
         for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
             const u32 row = i / VPR, c8 = i % VPR;
             const u64 src = (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8;
-            if constexpr (ROPE)
-                s_newk[row][c8] = cvt8_rope(sq.kin + (src - c8 * 8), c8 * 8, sq.pos + row,
-                                            p.rope.rdim, p.rope.theta, p.rope.neox);
-            else
+            if constexpr (ROPE) {
+                *(float4 *)(kf + row * D + c8 * 8) = *(const float4 *)(sq.kin + src);
+                *(float4 *)(kf + row * D + c8 * 8 + 4) = *(const float4 *)(sq.kin + src + 4);
+            } else {
                 s_newk[row][c8] = cvt8_f16(sq.kin + src);
+            }
             s_newv[row][c8] = cvt8_f16(sq.vin + src);
         }
     }
@@ -176,31 +184,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
             s_slot[i - kbeg] = s < sq.cap ? s : 0u;
         }
     }
-    /* q of the GQA group (RoPE'd when p.rope is set), scaled to log2 units,
-     * staged once per workgroup */
-    {
-        const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
+    /* q of the GQA group, scaled to log2 units, staged once per workgroup */
+    if constexpr (ROPE) {
+        for (int i = tid; i < G * D / 4; i += 256)
+            *(float4 *)(qf + i * 4) = *(const float4 *)(qb + i * 4);
+    } else {
         for (int i = tid; i < G * D / 8; i += 256) {
-            float t[8];
-            load8_rope(qb + (i / (D / 8)) * D, (i % (D / 8)) * 8, sq.pos + r,
-                       ROPE ? p.rope.rdim : 0u, p.rope.theta, p.rope.neox, t);
+            const float4 a = *(const float4 *)(qb + i * 8);
+            const float4 b = *(const float4 *)(qb + i * 8 + 4);
             const float sc = p.scale_log2;
-            s_q[i] = make_uint4(pack_f16x2_fast(t[0] * sc, t[1] * sc), pack_f16x2_fast(t[2] * sc, t[3] * sc),
-                                pack_f16x2_fast(t[4] * sc, t[5] * sc), pack_f16x2_fast(t[6] * sc, t[7] * sc));
+            s_q[i] = make_uint4(pack_f16x2_fast(a.x * sc, a.y * sc), pack_f16x2_fast(a.z * sc, a.w * sc),
+                                pack_f16x2_fast(b.x * sc, b.y * sc), pack_f16x2_fast(b.z * sc, b.w * sc));
         }
     }
     __syncthreads();
-    if (writer) {
-        for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
-            const u32 row = i / VPR, c8 = i % VPR;
-            const u32 key = sq.pos + row;
-            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
-            if (ph >= sq.cap) continue;
-            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
-            *(uint4 *)((u16 *)sq.k + dst) = s_newk[row][c8];
-            *(uint4 *)((u16 *)sq.v + dst) = s_newv[row][c8];
-        }
-    }
 
     /* q chunks of this lane's QK position, scaled to log2 units, f16 pairs */
     const int qc0 = (lane % LPK) * CPL;
@@ -260,7 +257,54 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
 
     const u32 ntile = (kend > kbeg) ? (kend - kbeg + TK - 1) / TK : 0;
     u32 ti = wave;
-    if (ti < ntile) TL_LOAD_TILE(kbeg + ti * TK);
+    /* the first tile's loads go out now; with ROPE a tile that holds new
+     * keys waits until they are converted */
+    const bool defer_first = ROPE && fused && kbeg + ti * TK + TK > sq.pos;
+    if (ti < ntile && !defer_first) TL_LOAD_TILE(kbeg + ti * TK);
+    if constexpr (ROPE) {
+        /* rotate q (G heads at pos + r) and the new K rows (at pos + row),
+         * one pair per thread, in place in LDS */
+        const u32 pairs = p.rope.rdim >> 1;
+        const u32 nq = G * pairs, nk = need_new ? p.rows_per_seq * pairs : 0u;
+        for (u32 t = tid; t < nq + nk; t += 256) {
+            const bool isq = t < nq;
+            const u32 tt = isq ? t : t - nq;
+            const u32 hrow = tt / pairs, i = tt % pairs;
+            float *row = (isq ? qf : kf) + hrow * D;
+            const u32 ia = p.rope.neox ? i : 2 * i, ib = p.rope.neox ? i + pairs : 2 * i + 1;
+            float c, sn, x, y;
+            rope_cs(i, p.rope.rdim, p.rope.theta, isq ? sq.pos + r : sq.pos + hrow, c, sn);
+            rope_rot(row[ia], row[ib], c, sn, x, y);
+            row[ia] = x;
+            row[ib] = y;
+        }
+        __syncthreads();
+        const float sc = p.scale_log2;
+        for (int i = tid; i < G * D / 8; i += 256) {
+            const float *t = qf + i * 8;
+            s_q[i] = make_uint4(pack_f16x2_fast(t[0] * sc, t[1] * sc), pack_f16x2_fast(t[2] * sc, t[3] * sc),
+                                pack_f16x2_fast(t[4] * sc, t[5] * sc), pack_f16x2_fast(t[6] * sc, t[7] * sc));
+        }
+        if (need_new)
+            for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
+                const float *t = kf + (i / VPR) * D + (i % VPR) * 8;
+                s_newk[i / VPR][i % VPR] = make_uint4(pack_f16x2(t[0], t[1]), pack_f16x2(t[2], t[3]),
+                                                      pack_f16x2(t[4], t[5]), pack_f16x2(t[6], t[7]));
+            }
+        __syncthreads();   /* also: qf/kf (tile memory) are free again */
+        if (ti < ntile && defer_first) TL_LOAD_TILE(kbeg + ti * TK);
+    }
+    if (writer) {
+        for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
+            const u32 row = i / VPR, c8 = i % VPR;
+            const u32 key = sq.pos + row;
+            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
+            if (ph >= sq.cap) continue;
+            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
+            *(uint4 *)((u16 *)sq.k + dst) = s_newk[row][c8];
+            *(uint4 *)((u16 *)sq.v + dst) = s_newv[row][c8];
+        }
+    }
     while (ti < ntile) {
         const u32 tbase = kbeg + ti * TK;
         if (tbase + TK <= kend) {
