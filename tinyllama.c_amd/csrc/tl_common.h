@@ -52,6 +52,8 @@ TL_DEV float dpp_f(float x) {
 #define DPP_QUAD_XOR2  0x4E   /* quad_perm [2,3,0,1] */
 #define DPP_ROW_HMIRROR 0x141 /* lane i <- lane 7-i within 8 */
 #define DPP_ROW_MIRROR  0x140 /* lane i <- lane 15-i within 16 */
+#define DPP_ROW_ROR4    0x124 /* lane i <- lane (i+4) % 16 within 16 (rotate) */
+#define DPP_ROW_ROR8    0x128 /* lane i <- lane (i+8) % 16 within 16 */
 
 /* Sum over aligned groups of N consecutive lanes (N in 1..64, power of 2);
  * every lane of a group receives the group total.  Within 16 lanes the moves

@@ -96,6 +96,33 @@ template <int D, int G>
 TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
                         float *s_hl);
 
+/* Optional per-workgroup timeline (measurement builds only, -DTL_DEC_TRACE):
+ * 16 u64 per workgroup: s_memrealtime (100 MHz) at launch entry (0),
+ * stream start (1), stream end (2), partial written (3), merge end (4),
+ * first tile in (5), epilogue LDS done (8), merge: counter seen (9),
+ * partials loaded (10); the XCC (6) and HW (7) ids. */
+#ifdef TL_DEC_TRACE
+__device__ u64 tl_dec_trace[8192 * 16];
+#define TL_TRACE(i)                                                                    \
+    do {                                                                               \
+        if (threadIdx.x == 0 && blockIdx.x < 8192)                                     \
+            tl_dec_trace[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime();      \
+    } while (0)
+#define TL_TRACE_IDS()                                                                 \
+    do {                                                                               \
+        if (threadIdx.x == 0 && blockIdx.x < 8192) {                                   \
+            tl_dec_trace[blockIdx.x * 16 + 6] = __builtin_amdgcn_s_getreg((3 << 11) | 20); \
+            tl_dec_trace[blockIdx.x * 16 + 7] = __builtin_amdgcn_s_getreg((31 << 11) | 4); \
+        }                                                                              \
+    } while (0)
+extern "C" int tl_dec_trace_read(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_dec_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#else
+#define TL_TRACE(i) do {} while (0)
+#define TL_TRACE_IDS() do {} while (0)
+#endif
+
 template <int D, int G, int TB, bool ROPE>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     using C = DCfg<D, TB>;
@@ -117,6 +144,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    TL_TRACE(0);
+    TL_TRACE_IDS();
 
     /* XCD-aware block order: block b runs on XCD b % 8; all splits of one
      * (row, kv-head) group land on the same XCD when the group count is a
@@ -198,6 +227,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
         }
     }
     __syncthreads();
+    TL_TRACE(1);
 
     /* q chunks of this lane's QK position, scaled to log2 units, f16 pairs */
     const int qc0 = (lane % LPK) * CPL;
@@ -324,10 +354,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
                 tv[j * 64 + lane] = b;
             }
         }
+#ifdef TL_DEC_TRACE
+        if (ti == 0 && lane == 0 && blockIdx.x < 8192)
+            tl_dec_trace[blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();
+#endif
         __builtin_amdgcn_wave_barrier();
         const u32 tnext = ti + 4;
         if (tnext < ntile) TL_LOAD_TILE(kbeg + tnext * TK);
 
+#ifdef TL_DEC_NOCOMPUTE
+        ti = tnext;
+        continue;
+#endif
         /* ---- scores: LPK lanes per key, CPL chunks each ---- */
         float sc[PASSES][G];
 #pragma unroll
@@ -438,6 +476,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
         }
     }
     __syncthreads();
+    TL_TRACE(2);
     float *s_acc = (float *)&s_kv[0][0][0];       /* [4][G][D] */
     {
         const int d0 = (lane % PVL) * DPL;
@@ -500,6 +539,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     __shared__ u32 s_last;
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    TL_TRACE(3);
     if (tid == 0)
         s_last = __hip_atomic_fetch_add(&p.counters[grp], 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
@@ -507,6 +547,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
     if (s_last != n_split - 1) return;
     if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     split_merge<D, G>(p, grow, kvh, si, r, (float *)&s_kv[0][0][0], &s_l[0][0]);
+#ifdef TL_DEC_TRACE
+    __syncthreads();
+    TL_TRACE(4);
+#endif
 }
 
 /* Merge of the n_split partials of one (row, kv-head) group inside the
@@ -570,6 +614,7 @@ TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, fl
         s_lv[i] = __uint_as_float(ml[1]);
     }
     __syncthreads();
+    TL_TRACE(10);
     for (int hh = wave; hh < G; hh += 4) {
         float mx = NEG_INF;
         for (u32 s = lane; s < ns; s += 64) mx = fmaxf(mx, s_w[hh * ns + s]);
@@ -710,6 +755,573 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p) {
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* Decode attention, LDS-direct ring                                        */
+/* ------------------------------------------------------------------------ */
+
+/* One 16-byte-per-lane load straight into LDS (global_load_lds_dwordx4,
+ * non-temporal: the cache is streamed once per step): lane i's 16 bytes land
+ * at LDS byte address m0 + 16*i.  Issued from inline
+ * assembly so the compiler does not wait for it before every LDS read; the
+ * caller waits with an explicit vmcnt.  `base` must be wave-uniform. */
+TL_DEV void lds_dma16(u32 m0, const void *base, u32 voff) {
+    const u64 g = (u64)base;
+    const u32 lo = __builtin_amdgcn_readfirstlane((u32)g);
+    const u32 hi = __builtin_amdgcn_readfirstlane((u32)(g >> 32));
+    const void *sb = (const void *)(((u64)hi << 32) | lo);
+    /* m0 is an input operand (the compiler writes it); s_nop covers the
+     * one-wait-state hazard between an M0 write and an LDS-direct load */
+    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                     :: "v"(voff), "s"(sb), "{m0}"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
+}
+
+/* wait until at most n tiles (8 loads each) are still in flight */
+TL_DEV void wait_tiles(u32 n) {
+    switch (n) {
+    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 2: __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    default: __asm__ volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    }
+}
+
+/* Ring-kernel tile geometry: a K (or V) tile is 4 KB; a lane owns 16
+ * consecutive dims (two 16-byte chunks) of one key in each of the tile's
+ * two passes, so LPK = D/16 lanes share a key and every lane holds one key
+ * pair (t, t + KPP) for the v_dot2 PV products. */
+template <int D>
+struct RCfg {
+    static constexpr int LPK = D / 16;       /* lanes per key */
+    static constexpr int KPP = 64 / LPK;     /* keys per pass */
+    static constexpr int TK = 2 * KPP;       /* keys per tile */
+    static constexpr int CPR = D / 8;        /* 16-byte chunks per row */
+    static constexpr int UNITS = TK * CPR;   /* 16-byte units per K (or V) tile */
+    static constexpr int LD = UNITS / 64;    /* loads per lane per K (or V) tile */
+};
+
+/* Lazy rescale margin (log2 units): the wave's running max (common to all
+ * its lanes) moves only when a score exceeds it by more than this, so
+ * probabilities stay <= 2^8 and most tiles skip the rescale. */
+#define TL_DEC_TAU 8.0f
+
+/* Scores, online softmax and PV of one staged tile (keys tbase..tbase+TK-1,
+ * those >= kend masked) into the lane group's running state (l, acc); the
+ * running max m is common to the wave.  Logical
+ * chunk c of tile row t sits at LDS unit t*CPR + (c ^ (t & 1)). */
+template <int D, int G>
+TL_DEV void ring_tile(const uint4 *tk, const uint4 *tv, const u32 (&qr)[G][8], u32 tbase,
+                      u32 kend, int lane, float (&m)[G], float (&l)[G], float (&acc)[G][16]) {
+    using C = RCfg<D>;
+    constexpr int LPK = C::LPK, KPP = C::KPP, CPR = C::CPR;
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    const int g = lane / LPK, sub = lane % LPK;
+    const int t0 = g, t1 = KPP + g;
+    const int c0 = (2 * sub) ^ (g & 1), c1 = (2 * sub + 1) ^ (g & 1);
+    const uint4 ka0 = tk[t0 * CPR + c0], ka1 = tk[t0 * CPR + c1];
+    const uint4 kb0 = tk[t1 * CPR + c0], kb1 = tk[t1 * CPR + c1];
+    const u32 ka[8] = {ka0.x, ka0.y, ka0.z, ka0.w, ka1.x, ka1.y, ka1.z, ka1.w};
+    const u32 kb[8] = {kb0.x, kb0.y, kb0.z, kb0.w, kb1.x, kb1.y, kb1.z, kb1.w};
+    float s0[G], s1[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            a = __builtin_amdgcn_fdot2(as_h2(ka[w]), as_h2(qr[h][w]), a, false);
+            b = __builtin_amdgcn_fdot2(as_h2(kb[w]), as_h2(qr[h][w]), b, false);
+        }
+        s0[h] = a;
+        s1[h] = b;
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        s0[h] = group_sum<LPK>(s0[h]);
+        s1[h] = group_sum<LPK>(s1[h]);
+        /* keep the sums unconditional (the compiler would otherwise move
+         * each dot-product chain into its own divergent branch) */
+        __asm__ volatile("" : "+v"(s0[h]), "+v"(s1[h]));
+    }
+    const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        s0[h] = v0 ? s0[h] : NEG_INF;
+        s1[h] = v1 ? s1[h] : NEG_INF;
+    }
+    const uint4 va0 = tv[t0 * CPR + c0], va1 = tv[t0 * CPR + c1];
+    const uint4 vb0 = tv[t1 * CPR + c0], vb1 = tv[t1 * CPR + c1];
+    u32 pp[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float mx = fmaxf(s0[h], s1[h]);
+        if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
+            /* rare: move the wave's common max to this tile's max */
+            const float mn = group_max<64>(mx);
+            const float alpha = fast_exp2(m[h] - mn);
+            l[h] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
+            m[h] = mn;
+        }
+        const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
+        const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
+        l[h] += p0 + p1;
+        pp[h] = pack_f16x2_fast(p0, p1);
+    }
+    const u32 va[8] = {va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
+    const u32 vb[8] = {vb0.x, vb0.y, vb0.z, vb0.w, vb1.x, vb1.y, vb1.z, vb1.w};
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        const half2_t lo = as_h2(perm_lo(va[w], vb[w]));   /* (V[t0][2w], V[t1][2w]) */
+        const half2_t hi = as_h2(perm_hi(va[w], vb[w]));
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            acc[h][2 * w] = __builtin_amdgcn_fdot2(lo, as_h2(pp[h]), acc[h][2 * w], false);
+            acc[h][2 * w + 1] = __builtin_amdgcn_fdot2(hi, as_h2(pp[h]), acc[h][2 * w + 1], false);
+        }
+    }
+}
+
+constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 : x >= 2 ? 2 : 1; }
+
+/* Merge of a group's n_split partials by its last workgroup, in registers:
+ * TPC threads per output float4 (h, d..d+3) each fold their share of the
+ * splits (all loads of a share requested at once, device-coherent) with an
+ * online max, then combine across the TPC lanes with DPP:
+ * out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s. */
+template <int D, int G, int NT>
+TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const DecSeq &sq) {
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    constexpr int COLS = G * D / 4;
+    constexpr int TPC = pow2_floor(NT / COLS > 16 ? 16 : (NT / COLS < 1 ? 1 : NT / COLS));
+    constexpr int K = 8;                       /* splits per load batch */
+    const int tid = threadIdx.x;
+    const u32 ns = p.n_split;
+    const __amdgpu_buffer_rsrc_t rml = buf_rsrc(p.ws_ml + pb);
+    const __amdgpu_buffer_rsrc_t racc = buf_rsrc(p.ws_acc + (u64)pb * D);
+    for (int col = tid / TPC; col < COLS; col += NT / TPC) {
+        const int part = tid % TPC;
+        const int h = col / (D / 4), d = (col % (D / 4)) * 4;
+        float M = NEG_INF, L = 0.f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (u32 s0 = part; s0 < ns; s0 += K * TPC) {
+            u32x2v_t ml[K];
+            u32x4v_t a[K];
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const u32 s = s0 + k * TPC;
+                const u32 pi = (u32)h * ns + (s < ns ? s : 0u);
+                ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rml, pi * 8, 0, TL_SC1);
+                a[k] = __builtin_amdgcn_raw_buffer_load_b128(racc, (pi * D + d) * 4, 0, TL_SC1);
+            }
+            float bm = NEG_INF;
+#pragma unroll
+            for (int k = 0; k < K; k++)
+                if (s0 + k * TPC < ns) bm = fmaxf(bm, __uint_as_float(ml[k][0]));
+            const float nm = fmaxf(M, bm);
+            const float mu = (nm == NEG_INF) ? 0.f : nm;
+            const float sc = fast_exp2(M - mu);
+            L *= sc;
+            O.x *= sc; O.y *= sc; O.z *= sc; O.w *= sc;
+            M = nm;
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const float w = (s0 + k * TPC < ns) ? fast_exp2(__uint_as_float(ml[k][0]) - mu) : 0.f;
+                L = fmaf(w, __uint_as_float(ml[k][1]), L);
+                O.x = fmaf(w, __uint_as_float(a[k][0]), O.x);
+                O.y = fmaf(w, __uint_as_float(a[k][1]), O.y);
+                O.z = fmaf(w, __uint_as_float(a[k][2]), O.z);
+                O.w = fmaf(w, __uint_as_float(a[k][3]), O.w);
+            }
+        }
+        if constexpr (TPC > 1) {
+            const float Mg = group_max<TPC>(M);
+            const float mu = (Mg == NEG_INF) ? 0.f : Mg;
+            const float e = fast_exp2(M - mu);
+            L = group_sum<TPC>(L * e);
+            O.x = group_sum<TPC>(O.x * e);
+            O.y = group_sum<TPC>(O.y * e);
+            O.z = group_sum<TPC>(O.z * e);
+            O.w = group_sum<TPC>(O.w * e);
+        }
+        if (part == 0) {
+            const float inv = 1.0f / L;
+            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)(kvh * G + h) * D + d] =
+                make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+        }
+    }
+}
+
+/* Decode attention with one workgroup of 8 waves per CU.  Each wave streams
+ * its tiles (every 8th tile of the chunk) through a ring of two LDS stages
+ * filled by LDS-direct loads: while one tile is computed the next is in
+ * flight, and two waves per SIMD hide each other's latency.  Every group of
+ * LPK lanes keeps its own online-softmax state (no cross-lane exchange in
+ * the stream loop); the groups and waves merge once at the end.  Split
+ * decomposition, XCD-aware block order, GQA sharing, the fused append and
+ * the split merge are those of attn_decode_kernel.  Tiles that hold rows
+ * appended by this launch (the last tiles of the last split) are filled
+ * from registers after the ring has drained. */
+#define TL_RING_WAVES 8
+#ifndef TL_XCD_ROT
+#define TL_XCD_ROT 0
+#endif
+#define TL_RING_STAGES 2
+template <int D, int G, bool ROPE>
+__global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
+    using C = RCfg<D>;
+    constexpr int LPK = C::LPK, CPR = C::CPR, TK = C::TK, UNITS = C::UNITS, LD = C::LD;
+    constexpr int W = TL_RING_WAVES, S = TL_RING_STAGES, NT = 64 * W;
+    constexpr int VPR = D / 8;
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    static_assert(LD == 4, "wait_tiles assumes 8 loads per tile");
+
+    __shared__ uint4 s_ring[W][S][2][UNITS];     /* per wave: S stages of (K, V) */
+    __shared__ u32 s_slot[TL_DEC_MAX_CHUNK];
+    __shared__ uint4 s_q[G * D / 8];
+    __shared__ float s_m[W][G];
+    __shared__ float s_l[W][G];
+    __shared__ uint4 s_newk[TL_DEC_MAX_NEW][D / 8];
+    __shared__ uint4 s_newv[TL_DEC_MAX_NEW][D / 8];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    TL_TRACE(0);
+    TL_TRACE_IDS();
+
+    const u32 n_split = p.n_split;
+    const u32 n_groups = gridDim.x / n_split;
+    const u32 bid = blockIdx.x;
+    u32 grp, split;
+    if ((n_groups & 7) == 0) {
+        const u32 xcd = bid & 7, local = bid >> 3;
+        grp = ((xcd + TL_XCD_ROT) & 7) + 8 * (local / n_split);
+        split = local % n_split;
+    } else {
+        grp = bid / n_split;
+        split = bid % n_split;
+    }
+    const u32 kvh = grp % p.n_kv;
+    const u32 grow = grp / p.n_kv;
+    const u32 si = grow / p.rows_per_seq;
+    const u32 r = grow % p.rows_per_seq;
+    const DecSeq sq = p.seq[si];
+
+    const u32 n_keys = sq.pos + r + 1;
+    const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
+    const u32 kbeg = start + split * p.chunk;
+    const u32 kend = min(kbeg + p.chunk, n_keys);
+    const bool fused = sq.kin != nullptr;
+    const bool writer = fused && split == 0 && r == 0;
+    const bool need_new = fused && (writer || kend > sq.pos);
+    const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
+
+    /* physical rows of the chunk's keys */
+    const bool staged = (sq.ring == 0) && (sq.slots != nullptr);
+    if (staged)
+        for (u32 i = kbeg + tid; i < kend; i += NT) {
+            const u32 s = sq.slots[i];
+            s_slot[i - kbeg] = s < sq.cap ? s : 0u;
+        }
+    /* q of the GQA group (RoPE'd at pos + r when ROPE), scaled to log2 units,
+     * f16; the launch's new K/V rows (K RoPE'd at pos + row), f16 */
+    const float sc = p.scale_log2;
+    if constexpr (ROPE) {
+        const u32 pairs = p.rope.rdim >> 1;
+        u16 *q16 = (u16 *)s_q;
+        for (u32 t = tid; t < (u32)G * (D / 2); t += NT) {
+            const u32 h = t / (D / 2), i = t % (D / 2);
+            const float *row = qb + h * D;
+            u32 ia, ib;
+            float x, y;
+            if (i < pairs) {
+                ia = p.rope.neox ? i : 2 * i;
+                ib = p.rope.neox ? i + pairs : 2 * i + 1;
+                float c, sn;
+                rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
+                rope_rot(row[ia], row[ib], c, sn, x, y);
+            } else {
+                ia = 2 * i;
+                ib = 2 * i + 1;
+                x = row[ia];
+                y = row[ib];
+            }
+            const u32 pk = pack_f16x2_fast(x * sc, y * sc);
+            q16[h * D + ia] = (u16)(pk & 0xffffu);
+            q16[h * D + ib] = (u16)(pk >> 16);
+        }
+        if (need_new) {
+            for (u32 t = tid; t < p.rows_per_seq * (D / 2); t += NT) {
+                const u32 row = t / (D / 2), i = t % (D / 2);
+                const float *src = sq.kin + (u64)row * sq.kv_stride + (u64)kvh * D;
+                u32 ia, ib;
+                float x, y;
+                if (i < pairs) {
+                    ia = p.rope.neox ? i : 2 * i;
+                    ib = p.rope.neox ? i + pairs : 2 * i + 1;
+                    float c, sn;
+                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + row, c, sn);
+                    rope_rot(src[ia], src[ib], c, sn, x, y);
+                } else {
+                    ia = 2 * i;
+                    ib = 2 * i + 1;
+                    x = src[ia];
+                    y = src[ib];
+                }
+                u16 *k16 = (u16 *)s_newk[row];
+                k16[ia] = (u16)f32_to_f16_bits(x);
+                k16[ib] = (u16)f32_to_f16_bits(y);
+            }
+            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
+                const u32 row = i / VPR, c8 = i % VPR;
+                s_newv[row][c8] = cvt8_f16(sq.vin + (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8);
+            }
+        }
+    } else {
+        for (int i = tid; i < G * D / 8; i += NT) {
+            const float4 a = *(const float4 *)(qb + i * 8);
+            const float4 b = *(const float4 *)(qb + i * 8 + 4);
+            s_q[i] = make_uint4(pack_f16x2_fast(a.x * sc, a.y * sc), pack_f16x2_fast(a.z * sc, a.w * sc),
+                                pack_f16x2_fast(b.x * sc, b.y * sc), pack_f16x2_fast(b.z * sc, b.w * sc));
+        }
+        if (need_new)
+            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
+                const u32 row = i / VPR, c8 = i % VPR;
+                const u64 src = (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8;
+                s_newk[row][c8] = cvt8_f16(sq.kin + src);
+                s_newv[row][c8] = cvt8_f16(sq.vin + src);
+            }
+    }
+    __syncthreads();
+    TL_TRACE(1);
+
+    const u16 *Kbase = sq.k + (u64)kvh * sq.cap * D;
+    const u16 *Vbase = sq.v + (u64)kvh * sq.cap * D;
+    const u32 ring_lds = (u32)(uintptr_t)&s_ring[wave][0][0][0];
+
+    /* tiles of the chunk: the first n_dma (entirely cache rows written
+     * before this launch) stream through the ring; the rest hold new rows */
+    const u32 ntile = (kend > kbeg) ? (kend - kbeg + TK - 1) / TK : 0;
+    u32 n_dma = ntile;
+    if (fused && kend > sq.pos) n_dma = sq.pos > kbeg ? (sq.pos - kbeg) / TK : 0;
+    const u32 nj = n_dma > (u32)wave ? (n_dma - wave + W - 1) / W : 0;   /* this wave's ring tiles */
+    const u32 klast = kend - 1;
+
+    auto phys = [&](u32 key) -> u32 {
+        if (sq.ring) return key % sq.ring;
+        return staged ? s_slot[key - kbeg] : key;
+    };
+    /* unit u = jj*64 + lane of a K (or V) tile holds chunk (u % CPR) ^ (row & 1)
+     * of tile row u / CPR.  Rows past the chunk load its last row (their
+     * scores are masked to -inf, so they add exactly 0). */
+    auto issue = [&](u32 j) {
+        const u32 tb = kbeg + (wave + W * j) * TK;
+        const u32 lk = ring_lds + (j % S) * (2 * UNITS * 16);
+#pragma unroll
+        for (int jj = 0; jj < LD; jj++) {
+            const int u = jj * 64 + lane;
+            const int row = u / CPR;
+            const u32 ph = phys(min(tb + (u32)row, klast));
+            const u32 off = (ph * D + (((u % CPR) ^ (row & 1)) * 8)) * 2;
+            lds_dma16(lk + jj * 1024, Kbase, off);
+            lds_dma16(lk + UNITS * 16 + jj * 1024, Vbase, off);
+        }
+    };
+
+    const u32 npre = nj < (u32)S ? nj : (u32)S;
+    for (u32 j = 0; j < npre; j++) issue(j);
+
+    /* q of this lane's 16 dims, every head of the group */
+    u32 qr[G][8];
+    {
+        const int sub = lane % LPK;
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const uint4 a = s_q[h * CPR + 2 * sub], b = s_q[h * CPR + 2 * sub + 1];
+            qr[h][0] = a.x; qr[h][1] = a.y; qr[h][2] = a.z; qr[h][3] = a.w;
+            qr[h][4] = b.x; qr[h][5] = b.y; qr[h][6] = b.z; qr[h][7] = b.w;
+        }
+    }
+    float m[G], l[G], acc[G][16];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        m[h] = NEG_INF;
+        l[h] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[h][e] = 0.f;
+    }
+
+    for (u32 j = 0; j < nj; j++) {
+        const u32 after = nj - 1 - j;
+        wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
+#ifdef TL_DEC_TRACE
+        if (j == 0 && lane == 0 && blockIdx.x < 8192)
+            tl_dec_trace[blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();
+#endif
+#ifndef TL_DEC_NOCOMPUTE
+        ring_tile<D, G>(s_ring[wave][j % S][0], s_ring[wave][j % S][1], qr,
+                        kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
+#endif
+        if (j + S < nj) issue(j + S);
+    }
+    /* tiles with new rows: cache rows and staged new rows through registers */
+    for (u32 t = n_dma + ((u32)wave + W - n_dma % W) % W; t < ntile; t += W) {
+        uint4 *tk = s_ring[wave][0][0];
+        uint4 *tv = s_ring[wave][0][1];
+        const u32 tb = kbeg + t * TK;
+#pragma unroll
+        for (int jj = 0; jj < LD; jj++) {
+            const int u = jj * 64 + lane;
+            const int row = u / CPR;
+            const u32 key = min(tb + (u32)row, klast);
+            const int c = (u % CPR) ^ (row & 1);
+            uint4 a, b;
+            if (key >= sq.pos) {
+                a = s_newk[key - sq.pos][c];
+                b = s_newv[key - sq.pos][c];
+            } else {
+                const u32 ph = phys(key);
+                a = ld_stream(Kbase + (u64)ph * D + c * 8);
+                b = ld_stream(Vbase + (u64)ph * D + c * 8);
+            }
+            tk[u] = a;
+            tv[u] = b;
+        }
+        __builtin_amdgcn_wave_barrier();
+        ring_tile<D, G>(tk, tv, qr, tb, kend, lane, m, l, acc);
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (writer) {
+        for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
+            const u32 row = i / VPR, c8 = i % VPR;
+            const u32 key = sq.pos + row;
+            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
+            if (ph >= sq.cap) continue;
+            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
+            *(uint4 *)((u16 *)sq.k + dst) = s_newk[row][c8];
+            *(uint4 *)((u16 *)sq.v + dst) = s_newv[row][c8];
+        }
+    }
+
+    /* ---- one state per workgroup and head ----
+     * The running max is wave-uniform, so the lanes of a wave add directly;
+     * the waves combine with weights exp2(m_w - M_h).  Every lane's acc goes
+     * to LDS (ring memory, float4 [head][k4][thread], batches of HB heads);
+     * TPC threads per output float4 each sum a share of the lanes and add
+     * across their quad with DPP. */
+    constexpr int HB = G < 4 ? G : 4;                 /* heads per LDS batch */
+    constexpr int COLB = HB * D / 4;                  /* float4 columns per batch */
+    constexpr int TPC = pow2_floor(NT / COLB > 16 ? 16 : NT / COLB);   /* threads per column */
+    constexpr int NLC = 64 / LPK * W;                 /* lanes per column (same sub) */
+    static_assert(TPC == 1 || TPC == 2 || TPC == 4 || TPC == 8 || TPC == 16, "TPC");
+    static_assert(NLC % TPC == 0, "lanes per thread");
+    static_assert(HB * 4 * NT * 16 <= (int)sizeof(s_ring), "epilogue exceeds the ring");
+    float4 *s_acc4 = (float4 *)&s_ring[0][0][0][0];
+    __syncthreads();                                  /* ring reads are done */
+    TL_TRACE(2);
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        /* l is replicated over the LPK lanes of a group */
+        const float lw = group_sum<64>(l[h]) * (1.0f / LPK);
+        if (lane == 0) {
+            s_m[wave][h] = m[h];
+            s_l[wave][h] = lw;
+        }
+    }
+    const bool single = (n_split == 1);
+    const bool last_merges = p.counters != nullptr;
+    const u32 pb = (grow * p.n_head + kvh * G) * n_split;
+#pragma unroll
+    for (int h0 = 0; h0 < G; h0 += HB) {
+        if (h0) __syncthreads();
+#pragma unroll
+        for (int hh = 0; hh < HB; hh++)
+            if (h0 + hh < G)
+#pragma unroll
+                for (int k4 = 0; k4 < 4; k4++)
+                    s_acc4[(hh * 4 + k4) * NT + tid] =
+                        make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
+                                    acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
+        __syncthreads();
+        if (h0 == 0) TL_TRACE(8);
+        const int col = tid / TPC, part = tid % TPC;
+        if (col < COLB && h0 + col / (D / 4) < G) {
+            const int hh = col / (D / 4), d = (col % (D / 4)) * 4;
+            const int h = h0 + hh;
+            const int csub = d / 16, k4 = (d % 16) / 4;
+            float mm = s_m[0][h];
+#pragma unroll
+            for (int w = 1; w < W; w++) mm = fmaxf(mm, s_m[w][h]);
+            const float mu = (mm == NEG_INF) ? 0.f : mm;
+            float L = 0.f;
+            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 *src = s_acc4 + (hh * 4 + k4) * NT + csub;
+#pragma unroll
+            for (int i = 0; i < NLC / TPC; i++) {
+                const int li = part + i * TPC;               /* lane index among NLC */
+                const int w = li / (64 / LPK), gi = li % (64 / LPK);
+                const float e = fast_exp2(s_m[w][h] - mu);
+                const float4 a = src[w * 64 + gi * LPK];
+                O.x = fmaf(e, a.x, O.x);
+                O.y = fmaf(e, a.y, O.y);
+                O.z = fmaf(e, a.z, O.z);
+                O.w = fmaf(e, a.w, O.w);
+            }
+#pragma unroll
+            for (int w = 0; w < W; w++) L += s_l[w][h] * fast_exp2(s_m[w][h] - mu);
+            O.x = group_sum<TPC>(O.x);
+            O.y = group_sum<TPC>(O.y);
+            O.z = group_sum<TPC>(O.z);
+            O.w = group_sum<TPC>(O.w);
+            if (part == 0) {
+                const u32 hq = kvh * G + h;
+                if (single) {
+                    const float inv = 1.0f / L;
+                    *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] =
+                        make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+                } else if (last_merges) {
+                    /* device-coherent stores: the merging workgroup may run
+                     * on another XCD and reads them with device-coherent loads */
+                    const u32 pi = (u32)h * n_split + split;
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        u32x4v_t{__float_as_uint(O.x), __float_as_uint(O.y), __float_as_uint(O.z),
+                                 __float_as_uint(O.w)},
+                        buf_rsrc(p.ws_acc + (u64)pb * D), (pi * D + d) * 4, 0, TL_SC1);
+                    if (d == 0)
+                        __builtin_amdgcn_raw_buffer_store_b64(
+                            u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
+                            buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
+                } else {
+                    const u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
+                    *(float4 *)&p.ws_acc[pi * D + d] = O;
+                    if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
+                }
+            }
+        }
+    }
+    if (single || !last_merges) return;
+
+    /* ---- the last split of this (row, kv-head) group to finish merges ----
+     * Its partial stores are complete (vmcnt 0) before the counter add, so
+     * the workgroup that sees n_split - 1 reads every partial. */
+    __shared__ u32 s_last;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    TL_TRACE(3);
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&p.counters[grp], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_last != n_split - 1) return;
+    if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    TL_TRACE(9);
+    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq);
+#ifdef TL_DEC_TRACE
+    __syncthreads();
+    TL_TRACE(4);
+#endif
+}
+
 /* One decode kernel instance: entry point and K (or V) bytes per wave tile
  * (the RoPE-fusing instances are separate so the plain ones carry none of
  * its code):
@@ -719,20 +1331,28 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p) {
 struct DecKernel {
     const void *fn;
     int tile_bytes;
+    int threads;
 };
+
+static u32 env_u32(const char *name, u32 dflt);
 
 template <int D>
 static DecKernel pick_kernel(int G, bool rope) {
+    const bool v1 = env_u32("TL_DECODE_V1", 0) != 0;
     switch (G) {
 #define TL_CASE(g)                                                                        \
     case g:                                                                               \
-        if (rope) return {(const void *)attn_decode_kernel<D, g, 4096, true>, 4096};      \
-        return {(const void *)attn_decode_kernel<D, g, 4096, false>, 4096};
+        if (!v1) {                                                                        \
+            if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true>, 4096, 64 * TL_RING_WAVES}; \
+            return {(const void *)attn_decode_ring_kernel<D, g, false>, 4096, 64 * TL_RING_WAVES};          \
+        }                                                                                 \
+        if (rope) return {(const void *)attn_decode_kernel<D, g, 4096, true>, 4096, 256}; \
+        return {(const void *)attn_decode_kernel<D, g, 4096, false>, 4096, 256};
         TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
         TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
 #undef TL_CASE
     default:
-        return {nullptr, 0};
+        return {nullptr, 0, 0};
     }
 }
 
@@ -756,14 +1376,14 @@ static int cu_count() {
 }
 
 /* resident workgroups per CU of a kernel (cached per entry point) */
-static int resident_per_cu(const void *fn) {
+static int resident_per_cu(const void *fn, int threads) {
     static const void *keys[64];
     static int vals[64];
     static int n = 0;
     for (int i = 0; i < n; i++)
         if (keys[i] == fn) return vals[i];
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, 256, 0) != hipSuccess || b < 1) b = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, threads, 0) != hipSuccess || b < 1) b = 1;
     if (n < 64) {
         keys[n] = fn;
         vals[n++] = b;
@@ -789,12 +1409,13 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     const u32 tk = (u32)K.tile_bytes / (2 * head_dim);   /* keys per wave tile */
     /* two workgroups per CU: measured best on MI355X for both tile sizes
      * (one resident wave of workgroups; more per CU only shortens chunks) */
-    int per_cu = resident_per_cu(K.fn);
+    int per_cu = resident_per_cu(K.fn, K.threads);
     if (per_cu > 2) per_cu = 2;
     const u32 target = env_u32("TL_DECODE_WGS", (u32)(per_cu * cu_count()));
     const u64 n_groups = (u64)n_rows_total * p.n_kv;
     u32 n_split = (u32)((target + n_groups - 1) / n_groups);
-    const u32 max_split = (max_vis + 4 * tk - 1) / (4 * tk);    /* >= one tile per wave */
+    const u32 waves = (u32)K.threads / 64;
+    const u32 max_split = (max_vis + waves * tk - 1) / (waves * tk);   /* >= one tile per wave */
     const u32 min_split = (max_vis + TL_DEC_MAX_CHUNK - 1) / TL_DEC_MAX_CHUNK;
     if (n_split > max_split) n_split = max_split;
     if (n_split < min_split) n_split = min_split;
@@ -818,7 +1439,7 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
         if (in_kernel_merge) p.counters = w->cnt;
     }
     void *args[] = {(void *)&p};
-    HIP_TRY(hipLaunchKernel(K.fn, dim3(n_split * (u32)n_groups), dim3(256), args, 0, st));
+    HIP_TRY(hipLaunchKernel(K.fn, dim3(n_split * (u32)n_groups), dim3(K.threads), args, 0, st));
     if (n_split == 1 || in_kernel_merge) return TL_OK;
     return tl_launch_merge(p, n_rows_total, head_dim, st);
 }

@@ -103,6 +103,10 @@ static int check_layer(const tl_kv_layer *L) {
     if (L->n_kv_head == 0 || L->cap == 0)
         return tl_fail(TL_EINVAL, "layer: empty shape");
     if (L->ring > L->cap) return tl_fail(TL_EINVAL, "ring %u > cap %u", L->ring, L->cap);
+    /* kernels address one kv-head's rows with 32-bit byte offsets */
+    if ((u64)L->cap * L->head_dim * sizeof(u16) > 0xFFFFFFFFull)
+        return tl_fail(TL_ERANGE, "layer: %u rows of head_dim %u exceed 4 GiB per kv-head",
+                       L->cap, L->head_dim);
     if (((uintptr_t)L->k | (uintptr_t)L->v) & 15)
         return tl_fail(TL_EINVAL, "cache storage not 16-byte aligned");
     return TL_OK;
