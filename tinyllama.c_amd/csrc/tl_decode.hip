@@ -59,22 +59,6 @@ TL_DEV uint4 ld_stream(const u16 *ptr) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int D, int TB>
-struct DCfg {
-    static constexpr int CPR = D / 8;           /* 16-byte chunks per row */
-    static constexpr int TK = TB / (2 * D);     /* keys per wave tile */
-    static constexpr int LPK = D / 32;          /* lanes per key in QK (4 chunks each) */
-    static constexpr int CPL = 4;               /* chunks per lane in QK */
-    static constexpr int KPP = 64 / LPK;        /* keys per QK pass */
-    static constexpr int PASSES = TK / KPP;     /* 1 or 2 */
-    static constexpr int UNITS = TK * CPR;      /* 512 units per tile */
-    static constexpr int LD = UNITS / 64;       /* 16-byte loads per lane per tile */
-    static constexpr int DPL = (D <= 128) ? 2 : 4;  /* PV dims per lane */
-    static constexpr int PVL = D / DPL;         /* lanes of one PV key group */
-    static constexpr int KG = 64 / PVL;         /* PV key groups per wave */
-    static constexpr int NPAIR = TK / 2;
-};
-
 TL_DEV u32 perm_lo(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 TL_DEV u32 perm_hi(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
@@ -91,10 +75,6 @@ TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
 /* Cache policy sc1: device-coherent access (written through to / read from
  * the level every XCD sees), the policy of agent-scope atomics. */
 #define TL_SC1 16
-
-template <int D, int G>
-TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
-                        float *s_hl);
 
 /* Optional per-workgroup timeline (measurement builds only, -DTL_DEC_TRACE):
  * 16 u64 per workgroup: s_memrealtime (100 MHz) at launch entry (0),
@@ -122,557 +102,6 @@ extern "C" int tl_dec_trace_read(void *host, size_t bytes) {
 #define TL_TRACE(i) do {} while (0)
 #define TL_TRACE_IDS() do {} while (0)
 #endif
-
-template <int D, int G, int TB, bool ROPE>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const DecParams p) {
-    using C = DCfg<D, TB>;
-    constexpr int CPR = C::CPR, TK = C::TK, LPK = C::LPK, CPL = C::CPL, KPP = C::KPP;
-    constexpr int PASSES = C::PASSES, UNITS = C::UNITS, LD = C::LD, DPL = C::DPL;
-    constexpr int PVL = C::PVL, KG = C::KG, NPAIR = C::NPAIR;
-    constexpr int GP = (G + 3) / 4 * 4;         /* p pairs padded to 16 bytes */
-    constexpr float NEG_INF = -__builtin_huge_valf();
-
-    __shared__ uint4 s_kv[4][2][UNITS];          /* per wave: K tile, V tile */
-    __shared__ u32 s_p[4][NPAIR][GP];            /* per wave: (p_t, p_t+1) f16 pairs */
-    __shared__ u32 s_slot[TL_DEC_MAX_CHUNK];
-    __shared__ uint4 s_q[G * D / 8];             /* q, f16, scaled to log2 units */
-    __shared__ float s_m[4][G];
-    __shared__ float s_l[4][G];
-    __shared__ uint4 s_newk[TL_DEC_MAX_NEW][D / 8];   /* new rows of a fused launch, f16 */
-    __shared__ uint4 s_newv[TL_DEC_MAX_NEW][D / 8];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    TL_TRACE(0);
-    TL_TRACE_IDS();
-
-    /* XCD-aware block order: block b runs on XCD b % 8; all splits of one
-     * (row, kv-head) group land on the same XCD when the group count is a
-     * multiple of 8, so the split merge reads partials from that XCD's L2. */
-    const u32 n_split = p.n_split;
-    const u32 n_groups = gridDim.x / n_split;
-    const u32 bid = blockIdx.x;
-    u32 grp, split;
-    if ((n_groups & 7) == 0) {
-        const u32 xcd = bid & 7, local = bid >> 3;
-        grp = xcd + 8 * (local / n_split);
-        split = local % n_split;
-    } else {
-        grp = bid / n_split;
-        split = bid % n_split;
-    }
-    const u32 kvh = grp % p.n_kv;
-    const u32 grow = grp / p.n_kv;
-    const u32 si = grow / p.rows_per_seq;
-    const u32 r = grow % p.rows_per_seq;
-    const DecSeq sq = p.seq[si];
-
-    const u32 n_keys = sq.pos + r + 1;
-    const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
-    const u32 kbeg = start + split * p.chunk;
-    const u32 kend = min(kbeg + p.chunk, n_keys);
-    /* fused append: the launch's new rows (positions pos..pos+rows-1, K
-     * RoPE'd when ROPE) are converted to f16 into LDS by every workgroup that
-     * reads one of them and by the split-0 workgroup of row 0, which also
-     * writes them to the cache.  No workgroup reads a cache row that is being
-     * written in this launch, and the stream loop never runs the conversion
-     * (or RoPE) code itself.
-     * With ROPE, q and the new K rows are first copied to LDS as f32, rotated
-     * one pair per thread while the first tile's loads are in flight, then
-     * converted. */
-    constexpr int VPR = D / 8;
-    const bool fused = sq.kin != nullptr;
-    const bool writer = fused && split == 0 && r == 0;
-    const bool need_new = fused && (writer || kend > sq.pos);
-    float *qf = (float *)&s_kv[0][0][0];             /* ROPE: [G][D] f32 */
-    float *kf = qf + G * D;                          /* ROPE: [rows][D] f32 */
-    const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
-    if (need_new) {
-        for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
-            const u32 row = i / VPR, c8 = i % VPR;
-            const u64 src = (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8;
-            if constexpr (ROPE) {
-                *(float4 *)(kf + row * D + c8 * 8) = *(const float4 *)(sq.kin + src);
-                *(float4 *)(kf + row * D + c8 * 8 + 4) = *(const float4 *)(sq.kin + src + 4);
-            } else {
-                s_newk[row][c8] = cvt8_f16(sq.kin + src);
-            }
-            s_newv[row][c8] = cvt8_f16(sq.vin + src);
-        }
-    }
-
-    /* physical rows of the chunk's keys, staged in LDS unless identity */
-    const bool staged = (sq.ring != 0) || (sq.slots != nullptr);
-    if (!staged) {
-    } else if (sq.ring) {
-        for (u32 i = kbeg + tid; i < kend; i += 256) s_slot[i - kbeg] = i % sq.ring;
-    } else if (sq.slots) {
-        for (u32 i = kbeg + tid; i < kend; i += 256) {
-            u32 s = sq.slots[i];
-            s_slot[i - kbeg] = s < sq.cap ? s : 0u;
-        }
-    }
-    /* q of the GQA group, scaled to log2 units, staged once per workgroup */
-    if constexpr (ROPE) {
-        for (int i = tid; i < G * D / 4; i += 256)
-            *(float4 *)(qf + i * 4) = *(const float4 *)(qb + i * 4);
-    } else {
-        for (int i = tid; i < G * D / 8; i += 256) {
-            const float4 a = *(const float4 *)(qb + i * 8);
-            const float4 b = *(const float4 *)(qb + i * 8 + 4);
-            const float sc = p.scale_log2;
-            s_q[i] = make_uint4(pack_f16x2_fast(a.x * sc, a.y * sc), pack_f16x2_fast(a.z * sc, a.w * sc),
-                                pack_f16x2_fast(b.x * sc, b.y * sc), pack_f16x2_fast(b.z * sc, b.w * sc));
-        }
-    }
-    __syncthreads();
-    TL_TRACE(1);
-
-    /* q chunks of this lane's QK position, scaled to log2 units, f16 pairs */
-    const int qc0 = (lane % LPK) * CPL;
-
-    float m[G], lsum[G], acc[G][DPL];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        m[h] = NEG_INF;
-        lsum[h] = 0.f;
-#pragma unroll
-        for (int e = 0; e < DPL; e++) acc[h][e] = 0.f;
-    }
-
-    const u16 *Kbase = sq.k + (u64)kvh * sq.cap * D;
-    const u16 *Vbase = sq.v + (u64)kvh * sq.cap * D;
-
-    uint4 *tk = s_kv[wave][0];
-    uint4 *tv = s_kv[wave][1];
-    u32 *tp = &s_p[wave][0][0];
-
-    /* register staging of one tile: K unit u = j*64 + lane holds chunk
-     * (u % CPR) ^ (row % CPR) of tile row u / CPR; V is stored unswizzled
-     * (unit u holds chunk u % CPR) because the PV phase reads whole rows.
-     * Keys past the chunk load the chunk's last row (always valid memory)
-     * and are zeroed when the tile is written to LDS. */
-    uint4 rk[LD], rv[LD];
-#define TL_PHYS(key) (staged ? s_slot[(key) - kbeg] : (key))
-#define TL_LOAD_TILE(TBASE)                                                         \
-    do {                                                                            \
-        const u32 tb_ = (TBASE), klast_ = kend - 1;                                 \
-        if (fused && tb_ + TK > sq.pos) {   /* tile holds new keys */               \
-            _Pragma("unroll") for (int j = 0; j < LD; j++) {                        \
-                const int u = j * 64 + lane;                                        \
-                const int row = u / CPR;                                            \
-                const u32 key = min(tb_ + (u32)row, klast_);                        \
-                const int kc_ = (u % CPR) ^ (row % CPR), vc_ = u % CPR;             \
-                if (key >= sq.pos) {                                                \
-                    rk[j] = s_newk[key - sq.pos][kc_];                              \
-                    rv[j] = s_newv[key - sq.pos][vc_];                              \
-                } else {                                                            \
-                    const u32 ph = TL_PHYS(key);                                    \
-                    rk[j] = ld_stream(Kbase + (u64)ph * D + kc_ * 8);               \
-                    rv[j] = ld_stream(Vbase + (u64)ph * D + vc_ * 8);               \
-                }                                                                   \
-            }                                                                       \
-            break;                                                                  \
-        }                                                                           \
-        _Pragma("unroll") for (int j = 0; j < LD; j++) {                            \
-            const int u = j * 64 + lane;                                            \
-            const int row = u / CPR;                                                \
-            const u32 key = min(tb_ + (u32)row, klast_);                            \
-            const u32 ph = TL_PHYS(key);                                            \
-            rk[j] = ld_stream(Kbase + (u64)ph * D + ((u % CPR) ^ (row % CPR)) * 8); \
-            rv[j] = ld_stream(Vbase + (u64)ph * D + (u % CPR) * 8);                 \
-        }                                                                           \
-    } while (0)
-
-    const u32 ntile = (kend > kbeg) ? (kend - kbeg + TK - 1) / TK : 0;
-    u32 ti = wave;
-    /* the first tile's loads go out now; with ROPE a tile that holds new
-     * keys waits until they are converted */
-    const bool defer_first = ROPE && fused && kbeg + ti * TK + TK > sq.pos;
-    if (ti < ntile && !defer_first) TL_LOAD_TILE(kbeg + ti * TK);
-    if constexpr (ROPE) {
-        /* rotate q (G heads at pos + r) and the new K rows (at pos + row),
-         * one pair per thread, in place in LDS */
-        const u32 pairs = p.rope.rdim >> 1;
-        const u32 nq = G * pairs, nk = need_new ? p.rows_per_seq * pairs : 0u;
-        for (u32 t = tid; t < nq + nk; t += 256) {
-            const bool isq = t < nq;
-            const u32 tt = isq ? t : t - nq;
-            const u32 hrow = tt / pairs, i = tt % pairs;
-            float *row = (isq ? qf : kf) + hrow * D;
-            const u32 ia = p.rope.neox ? i : 2 * i, ib = p.rope.neox ? i + pairs : 2 * i + 1;
-            float c, sn, x, y;
-            rope_cs(i, p.rope.rdim, p.rope.theta, isq ? sq.pos + r : sq.pos + hrow, c, sn);
-            rope_rot(row[ia], row[ib], c, sn, x, y);
-            row[ia] = x;
-            row[ib] = y;
-        }
-        __syncthreads();
-        const float sc = p.scale_log2;
-        for (int i = tid; i < G * D / 8; i += 256) {
-            const float *t = qf + i * 8;
-            s_q[i] = make_uint4(pack_f16x2_fast(t[0] * sc, t[1] * sc), pack_f16x2_fast(t[2] * sc, t[3] * sc),
-                                pack_f16x2_fast(t[4] * sc, t[5] * sc), pack_f16x2_fast(t[6] * sc, t[7] * sc));
-        }
-        if (need_new)
-            for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
-                const float *t = kf + (i / VPR) * D + (i % VPR) * 8;
-                s_newk[i / VPR][i % VPR] = make_uint4(pack_f16x2(t[0], t[1]), pack_f16x2(t[2], t[3]),
-                                                      pack_f16x2(t[4], t[5]), pack_f16x2(t[6], t[7]));
-            }
-        __syncthreads();   /* also: qf/kf (tile memory) are free again */
-        if (ti < ntile && defer_first) TL_LOAD_TILE(kbeg + ti * TK);
-    }
-    if (writer) {
-        for (u32 i = tid; i < p.rows_per_seq * VPR; i += 256) {
-            const u32 row = i / VPR, c8 = i % VPR;
-            const u32 key = sq.pos + row;
-            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
-            if (ph >= sq.cap) continue;
-            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
-            *(uint4 *)((u16 *)sq.k + dst) = s_newk[row][c8];
-            *(uint4 *)((u16 *)sq.v + dst) = s_newv[row][c8];
-        }
-    }
-    while (ti < ntile) {
-        const u32 tbase = kbeg + ti * TK;
-        if (tbase + TK <= kend) {
-#pragma unroll
-            for (int j = 0; j < LD; j++) {
-                tk[j * 64 + lane] = rk[j];
-                tv[j * 64 + lane] = rv[j];
-            }
-        } else {   /* tail tile: rows past kend contribute exactly 0 */
-#pragma unroll
-            for (int j = 0; j < LD; j++) {
-                const bool ok = tbase + (u32)((j * 64 + lane) / CPR) < kend;
-                uint4 a = rk[j], b = rv[j];
-                a.x = ok ? a.x : 0u; a.y = ok ? a.y : 0u; a.z = ok ? a.z : 0u; a.w = ok ? a.w : 0u;
-                b.x = ok ? b.x : 0u; b.y = ok ? b.y : 0u; b.z = ok ? b.z : 0u; b.w = ok ? b.w : 0u;
-                tk[j * 64 + lane] = a;
-                tv[j * 64 + lane] = b;
-            }
-        }
-#ifdef TL_DEC_TRACE
-        if (ti == 0 && lane == 0 && blockIdx.x < 8192)
-            tl_dec_trace[blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();
-#endif
-        __builtin_amdgcn_wave_barrier();
-        const u32 tnext = ti + 4;
-        if (tnext < ntile) TL_LOAD_TILE(kbeg + tnext * TK);
-
-#ifdef TL_DEC_NOCOMPUTE
-        ti = tnext;
-        continue;
-#endif
-        /* ---- scores: LPK lanes per key, CPL chunks each ---- */
-        float sc[PASSES][G];
-#pragma unroll
-        for (int ps = 0; ps < PASSES; ps++) {
-            const int kt = ps * KPP + lane / LPK;
-            float d[G];
-#pragma unroll
-            for (int h = 0; h < G; h++) d[h] = 0.f;
-#pragma unroll
-            for (int j = 0; j < CPL; j++) {
-                const int c = qc0 + j;
-                const uint4 kv = tk[kt * CPR + (c ^ (kt % CPR))];
-#pragma unroll
-                for (int h = 0; h < G; h++) {
-                    const uint4 qv = s_q[h * CPR + c];
-                    d[h] = __builtin_amdgcn_fdot2(as_h2(kv.x), as_h2(qv.x), d[h], false);
-                    d[h] = __builtin_amdgcn_fdot2(as_h2(kv.y), as_h2(qv.y), d[h], false);
-                    d[h] = __builtin_amdgcn_fdot2(as_h2(kv.z), as_h2(qv.z), d[h], false);
-                    d[h] = __builtin_amdgcn_fdot2(as_h2(kv.w), as_h2(qv.w), d[h], false);
-                }
-            }
-            const bool valid = tbase + kt < kend;
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-                float t = group_sum<LPK>(d[h]);
-                sc[ps][h] = valid ? t : NEG_INF;
-            }
-        }
-
-        /* ---- online softmax over the tile (wave-uniform max) ---- */
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            float tm = sc[0][h];
-#pragma unroll
-            for (int ps = 1; ps < PASSES; ps++) tm = fmaxf(tm, sc[ps][h]);
-            tm = group_max<64>(tm);
-            const float mn = fmaxf(m[h], tm);
-            const float mu = (mn == NEG_INF) ? 0.f : mn;
-            const float alpha = fast_exp2(m[h] - mu);
-            m[h] = mn;
-            float ls = lsum[h] * alpha;
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[h][e] *= alpha;
-#pragma unroll
-            for (int ps = 0; ps < PASSES; ps++) {
-                const float pr = fast_exp2(sc[ps][h] - mu);
-                ls += pr;
-                /* pair keys (2i, 2i+1): lane groups gi and gi+1 */
-                const float pn = __shfl_xor(pr, LPK);
-                const int gi = lane / LPK;
-                if ((gi & 1) == 0 && (lane % LPK) == 0) {
-                    const int kt = ps * KPP + gi;
-                    tp[(kt >> 1) * GP + h] = pack_f16x2_fast(pr, pn);
-                }
-            }
-            lsum[h] = ls;
-        }
-        __builtin_amdgcn_wave_barrier();
-
-        /* ---- PV: lanes own DPL dims, v_dot2 over key pairs ---- */
-        const int kg = lane / PVL;
-        const int d0 = (lane % PVL) * DPL;
-        const int vc = d0 / 8;
-        const int vw = (d0 % 8) / 2;
-#pragma unroll
-        for (int ip = 0; ip < NPAIR / KG; ip++) {
-            const int pi = ip * KG + kg;
-            const int t0 = 2 * pi, t1 = 2 * pi + 1;
-            const u32 *r0 = (const u32 *)&tv[t0 * CPR + vc] + vw;
-            const u32 *r1 = (const u32 *)&tv[t1 * CPR + vc] + vw;
-            u32 a[DPL / 2], b[DPL / 2];
-#pragma unroll
-            for (int w = 0; w < DPL / 2; w++) {
-                a[w] = r0[w];
-                b[w] = r1[w];
-            }
-            u32 pp[GP];
-#pragma unroll
-            for (int g4 = 0; g4 < GP; g4 += 4) {
-                const uint4 t = *(const uint4 *)&tp[pi * GP + g4];
-                pp[g4] = t.x; pp[g4 + 1] = t.y; pp[g4 + 2] = t.z; pp[g4 + 3] = t.w;
-            }
-#pragma unroll
-            for (int w = 0; w < DPL / 2; w++) {
-                const half2_t lo = as_h2(perm_lo(a[w], b[w]));
-                const half2_t hi = as_h2(perm_hi(a[w], b[w]));
-#pragma unroll
-                for (int h = 0; h < G; h++) {
-                    acc[h][2 * w] = __builtin_amdgcn_fdot2(lo, as_h2(pp[h]), acc[h][2 * w], false);
-                    acc[h][2 * w + 1] = __builtin_amdgcn_fdot2(hi, as_h2(pp[h]), acc[h][2 * w + 1], false);
-                }
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-        ti = tnext;
-    }
-
-#undef TL_LOAD_TILE
-#undef TL_PHYS
-
-    /* ---- wave state -> LDS (tile memory is reused after the barrier) ---- */
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        lsum[h] = group_sum<64>(lsum[h]) * (1.0f / LPK);
-        if constexpr (KG > 1) {
-#pragma unroll
-            for (int e = 0; e < DPL; e++) acc[h][e] += __shfl_xor(acc[h][e], PVL);
-        }
-    }
-    __syncthreads();
-    TL_TRACE(2);
-    float *s_acc = (float *)&s_kv[0][0][0];       /* [4][G][D] */
-    {
-        const int d0 = (lane % PVL) * DPL;
-        if (lane < PVL) {
-#pragma unroll
-            for (int h = 0; h < G; h++)
-#pragma unroll
-                for (int e = 0; e < DPL; e++) s_acc[(wave * G + h) * D + d0 + e] = acc[h][e];
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-                s_m[wave][h] = m[h];
-                s_l[wave][h] = lsum[h];
-            }
-        }
-    }
-    __syncthreads();
-
-    /* ---- merge the 4 waves; write the final row or this split's partial ---- */
-    const bool single = (n_split == 1);
-    const bool last_merges = p.counters != nullptr;
-    for (int o = tid; o < G * D; o += 256) {
-        const int h = o / D, d = o % D;
-        float mm = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
-        float mu = (mm == NEG_INF) ? 0.f : mm;
-        float L = 0.f, O = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            float f = fast_exp2(s_m[w][h] - mu);
-            L += s_l[w][h] * f;
-            O += s_acc[(w * G + h) * D + d] * f;
-        }
-        const u32 hq = kvh * G + h;
-        if (single) {
-            sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] = O / L;
-        } else if (last_merges) {
-            /* device-coherent stores: the merging workgroup may run on
-             * another XCD and reads them with device-coherent loads */
-            const u32 pb = ((grow * p.n_head + kvh * G) * n_split) ;
-            const u32 pi = (u32)h * n_split + split;
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O),
-                                                  buf_rsrc(p.ws_acc + (u64)pb * D),
-                                                  (pi * D + d) * 4, 0, TL_SC1);
-            if (d == 0)
-                __builtin_amdgcn_raw_buffer_store_b64(
-                    u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
-                    buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
-        } else {
-            u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
-            p.ws_acc[pi * D + d] = O;
-            if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
-        }
-    }
-    if (single || !last_merges) return;
-
-    /* ---- the last split of this (row, kv-head) group to finish merges ----
-     * Its partial stores are complete (vmcnt 0) before the counter add, so
-     * the workgroup that sees n_split - 1 reads every partial. */
-    __shared__ u32 s_last;
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    TL_TRACE(3);
-    if (tid == 0)
-        s_last = __hip_atomic_fetch_add(&p.counters[grp], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_last != n_split - 1) return;
-    if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    split_merge<D, G>(p, grow, kvh, si, r, (float *)&s_kv[0][0][0], &s_l[0][0]);
-#ifdef TL_DEC_TRACE
-    __syncthreads();
-    TL_TRACE(4);
-#endif
-}
-
-/* Merge of the n_split partials of one (row, kv-head) group inside the
- * decode launch: weights w_s = exp2(m_s - M) per head, O = sum w_s acc_s,
- * out = O / sum w_s l_s.  Up to 32 partial float4 per thread and all (m, l)
- * pairs are requested together, so the common case costs one round trip
- * to memory; larger merges stream in batches.  lds: >= 2*G*n_split + 4*256
- * floats. */
-template <int D, int G>
-TL_DEV void split_merge(const DecParams &p, u32 grow, u32 kvh, u32 si, u32 r, float *lds,
-                        float *s_hl) {
-    constexpr float NEG_INF = -__builtin_huge_valf();
-    constexpr int COLS = G * D / 4;                       /* float4 columns */
-    constexpr int SUBS = COLS >= 256 ? 1 : 256 / COLS;    /* thread subsets over splits */
-    constexpr int NIT = (COLS * SUBS + 255) / 256;        /* columns per thread */
-    constexpr int BIG = 32 / NIT;    /* partials per column when all fit in one request wave */
-    constexpr int B = 8 / NIT;       /* partials per column per batch otherwise */
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const u32 ns = p.n_split;
-    const u32 pb = (grow * p.n_head + kvh * G) * ns;
-    const __amdgpu_buffer_rsrc_t rml = buf_rsrc(p.ws_ml + pb);
-    const __amdgpu_buffer_rsrc_t racc = buf_rsrc(p.ws_acc + (u64)pb * D);
-    float *s_w = lds;                 /* [G][ns] max, then weight */
-    float *s_lv = lds + G * ns;       /* [G][ns] sums */
-    float4 *s_part = (float4 *)(lds + 2 * G * ns + ((2 * G * ns) & 3 ? 4 - ((2 * G * ns) & 3) : 0));
-
-    /* thread column k: it = tid + 256 k -> head h, dims (col % (D/4)) * 4,
-     * splits sub, sub + SUBS, ... */
-#define TL_COL(k)                                                                     \
-    const int it = tid + (k) * 256;                                                   \
-    const int col = it % COLS, sub = it / COLS;                                       \
-    const bool live = it < COLS * SUBS;                                               \
-    const u32 cb = (u32)(col / (D / 4)) * ns * D + (u32)(col % (D / 4)) * 4;          \
-    const int h = col / (D / 4);                                                      \
-    (void)h; (void)cb; (void)live
-#define TL_LOAD(dst, s) \
-    dst = (live && (s) < ns) ? __builtin_amdgcn_raw_buffer_load_b128(racc, (cb + (s) * D) * 4, 0, TL_SC1) \
-                             : u32x4v_t{0u, 0u, 0u, 0u}
-#define TL_FMA(a, v, s)                                                               \
-    do {                                                                              \
-        const float w_ = (live && (s) < ns) ? s_w[h * ns + (s)] : 0.f;                \
-        a.x = fmaf(w_, __uint_as_float(v[0]), a.x);                                   \
-        a.y = fmaf(w_, __uint_as_float(v[1]), a.y);                                   \
-        a.z = fmaf(w_, __uint_as_float(v[2]), a.z);                                   \
-        a.w = fmaf(w_, __uint_as_float(v[3]), a.w);                                   \
-    } while (0)
-
-    const bool one_wave = ns <= (u32)(SUBS * BIG);
-    u32x4v_t v[NIT][BIG];
-    if (one_wave) {
-#pragma unroll
-        for (int k = 0; k < NIT; k++) {
-            TL_COL(k);
-#pragma unroll
-            for (int b = 0; b < BIG; b++) TL_LOAD(v[k][b], sub + b * SUBS);
-        }
-    }
-    for (u32 i = tid; i < G * ns; i += 256) {
-        const u32x2v_t ml = __builtin_amdgcn_raw_buffer_load_b64(rml, i * 8, 0, TL_SC1);
-        s_w[i] = __uint_as_float(ml[0]);
-        s_lv[i] = __uint_as_float(ml[1]);
-    }
-    __syncthreads();
-    TL_TRACE(10);
-    for (int hh = wave; hh < G; hh += 4) {
-        float mx = NEG_INF;
-        for (u32 s = lane; s < ns; s += 64) mx = fmaxf(mx, s_w[hh * ns + s]);
-        mx = group_max<64>(mx);
-        const float mu = (mx == NEG_INF) ? 0.f : mx;
-        float L = 0.f;
-        for (u32 s = lane; s < ns; s += 64) {
-            const float w = fast_exp2(s_w[hh * ns + s] - mu);
-            s_w[hh * ns + s] = w;
-            L += w * s_lv[hh * ns + s];
-        }
-        L = group_sum<64>(L);
-        if (lane == 0) s_hl[hh] = L;
-    }
-    __syncthreads();
-    float4 acc[NIT];
-#pragma unroll
-    for (int k = 0; k < NIT; k++) {
-        acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        TL_COL(k);
-        if (one_wave) {
-#pragma unroll
-            for (int b = 0; b < BIG; b++) TL_FMA(acc[k], v[k][b], sub + b * SUBS);
-        } else {
-            for (u32 s0 = sub; s0 < ns; s0 += B * SUBS) {
-                u32x4v_t t[B];
-#pragma unroll
-                for (int b = 0; b < B; b++) TL_LOAD(t[b], s0 + b * SUBS);
-#pragma unroll
-                for (int b = 0; b < B; b++) TL_FMA(acc[k], t[b], s0 + b * SUBS);
-            }
-        }
-    }
-#undef TL_COL
-#undef TL_LOAD
-#undef TL_FMA
-#pragma unroll
-    for (int k = 0; k < NIT; k++) {
-        const int it = tid + k * 256;
-        if (it < COLS * SUBS) s_part[(it / COLS) * COLS + it % COLS] = acc[k];
-    }
-    __syncthreads();
-    const DecSeq &sq = p.seq[si];
-    for (int col = tid; col < COLS; col += 256) {
-        float4 o = s_part[col];
-        for (int sb = 1; sb < SUBS; sb++) {
-            const float4 t = s_part[sb * COLS + col];
-            o.x += t.x; o.y += t.y; o.z += t.z; o.w += t.w;
-        }
-        const int h = col / (D / 4), d = (col % (D / 4)) * 4;
-        const float inv = 1.0f / s_hl[h];
-        float *dst = sq.dst + (u64)r * p.q_stride + (u64)(kvh * G + h) * D + d;
-        dst[0] = o.x * inv;
-        dst[1] = o.y * inv;
-        dst[2] = o.z * inv;
-        dst[3] = o.w * inv;
-    }
-}
 
 /* Split merge as its own launch (no cross-workgroup synchronisation inside
  * the decode kernel).  grid = rows * n_head, 256 threads.  Weights
@@ -885,11 +314,13 @@ constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 
 
 /* Merge of a group's n_split partials by its last workgroup, in registers:
  * TPC threads per output float4 (h, d..d+3) each fold their share of the
- * splits (all loads of a share requested at once, device-coherent) with an
- * online max, then combine across the TPC lanes with DPP:
- * out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s. */
+ * splits with an online max, then combine across the TPC lanes with DPP:
+ * out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s.  The first
+ * batch of partial rows and every (m, l) pair are requested together
+ * (device-coherent loads); the pairs go through LDS (s_ml: G*n_split). */
 template <int D, int G, int NT>
-TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const DecSeq &sq) {
+TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const DecSeq &sq,
+                             float2 *s_ml) {
     constexpr float NEG_INF = -__builtin_huge_valf();
     constexpr int COLS = G * D / 4;
     constexpr int TPC = pow2_floor(NT / COLS > 16 ? 16 : (NT / COLS < 1 ? 1 : NT / COLS));
@@ -898,25 +329,42 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
     const u32 ns = p.n_split;
     const __amdgpu_buffer_rsrc_t rml = buf_rsrc(p.ws_ml + pb);
     const __amdgpu_buffer_rsrc_t racc = buf_rsrc(p.ws_acc + (u64)pb * D);
-    for (int col = tid / TPC; col < COLS; col += NT / TPC) {
-        const int part = tid % TPC;
+    const int part = tid % TPC;
+    const int col0 = tid / TPC;
+    u32x4v_t a[K];
+    auto load_batch = [&](int col, u32 s0) {
         const int h = col / (D / 4), d = (col % (D / 4)) * 4;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const u32 s = min(s0 + k * TPC, ns - 1);
+            const u32 off = (((u32)h * ns + s) * D + d) * 4;
+            a[k] = __builtin_amdgcn_raw_buffer_load_b128(racc, off, 0, TL_SC1);
+        }
+    };
+    if (col0 < COLS) load_batch(col0, (u32)part);
+    for (u32 i = tid; i < (u32)G * ns; i += NT) {
+        const u32x2v_t ml = __builtin_amdgcn_raw_buffer_load_b64(rml, i * 8, 0, TL_SC1);
+        s_ml[i] = make_float2(__uint_as_float(ml[0]), __uint_as_float(ml[1]));
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    TL_TRACE(10);
+    for (int col = col0; col < COLS; col += NT / TPC) {
+        const int h = col / (D / 4), d = (col % (D / 4)) * 4;
+        const float2 *mlh = s_ml + (u32)h * ns;
         float M = NEG_INF, L = 0.f;
         float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
         for (u32 s0 = part; s0 < ns; s0 += K * TPC) {
-            u32x2v_t ml[K];
-            u32x4v_t a[K];
+            if (col != col0 || s0 != (u32)part) load_batch(col, s0);
+            float2 ml[K];
+            float bm = NEG_INF;
 #pragma unroll
             for (int k = 0; k < K; k++) {
                 const u32 s = s0 + k * TPC;
-                const u32 pi = (u32)h * ns + (s < ns ? s : 0u);
-                ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rml, pi * 8, 0, TL_SC1);
-                a[k] = __builtin_amdgcn_raw_buffer_load_b128(racc, (pi * D + d) * 4, 0, TL_SC1);
+                ml[k] = mlh[min(s, ns - 1)];
+                if (s >= ns) ml[k] = make_float2(NEG_INF, 0.f);   /* past the last split */
+                bm = fmaxf(bm, ml[k].x);
             }
-            float bm = NEG_INF;
-#pragma unroll
-            for (int k = 0; k < K; k++)
-                if (s0 + k * TPC < ns) bm = fmaxf(bm, __uint_as_float(ml[k][0]));
             const float nm = fmaxf(M, bm);
             const float mu = (nm == NEG_INF) ? 0.f : nm;
             const float sc = fast_exp2(M - mu);
@@ -925,8 +373,8 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
             M = nm;
 #pragma unroll
             for (int k = 0; k < K; k++) {
-                const float w = (s0 + k * TPC < ns) ? fast_exp2(__uint_as_float(ml[k][0]) - mu) : 0.f;
-                L = fmaf(w, __uint_as_float(ml[k][1]), L);
+                const float w = fast_exp2(ml[k].x - mu);
+                L = fmaf(w, ml[k].y, L);
                 O.x = fmaf(w, __uint_as_float(a[k][0]), O.x);
                 O.y = fmaf(w, __uint_as_float(a[k][1]), O.y);
                 O.z = fmaf(w, __uint_as_float(a[k][2]), O.z);
@@ -1205,75 +653,88 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     /* ---- one state per workgroup and head ----
      * The running max is wave-uniform, so the lanes of a wave add directly;
-     * the waves combine with weights exp2(m_w - M_h).  Every lane's acc goes
-     * to LDS (ring memory, float4 [head][k4][thread], batches of HB heads);
-     * TPC threads per output float4 each sum a share of the lanes and add
-     * across their quad with DPP. */
-    constexpr int HB = G < 4 ? G : 4;                 /* heads per LDS batch */
-    constexpr int COLB = HB * D / 4;                  /* float4 columns per batch */
-    constexpr int TPC = pow2_floor(NT / COLB > 16 ? 16 : NT / COLB);   /* threads per column */
-    constexpr int NLC = 64 / LPK * W;                 /* lanes per column (same sub) */
-    static_assert(TPC == 1 || TPC == 2 || TPC == 4 || TPC == 8 || TPC == 16, "TPC");
-    static_assert(NLC % TPC == 0, "lanes per thread");
-    static_assert(HB * 4 * NT * 16 <= (int)sizeof(s_ring), "epilogue exceeds the ring");
-    float4 *s_acc4 = (float4 *)&s_ring[0][0][0][0];
-    __syncthreads();                                  /* ring reads are done */
-    TL_TRACE(2);
+     * the waves combine with weights exp2(m_w - M_h).  A wave that has
+     * finished its tiles writes its state into its own ring region (no
+     * barrier: that region is no longer read): acc as float4
+     * [head][k4][lane] (up to HB heads, 16 KB), l per lane group.  After
+     * one barrier, TPC threads per output float4 each add a share of the
+     * W * GPW lane groups (lanes sub + LPK*part: every 8-lane phase of a
+     * read touches distinct banks), then add across with shuffles.  More
+     * than HB heads take further rounds through the same memory. */
+    constexpr int GPW = 64 / LPK;                     /* lane groups per wave */
+    constexpr int NGRP = W * GPW;                     /* lane groups per workgroup */
+    constexpr int HB = G < 4 ? G : 4;                 /* heads per round */
+    constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
+    constexpr int TPC0 = NT / COLB > GPW ? GPW : NT / COLB;
+    constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
+    constexpr int WREG = S * 2 * UNITS;               /* float4 per wave region */
+    static_assert(HB * 4 * 64 <= WREG, "wave state exceeds its ring region");
+    static_assert(GPW % TPC == 0, "lane groups per thread");
+    __shared__ float s_lg[G][NGRP];
+    float4 *s_w4 = (float4 *)&s_ring[0][0][0][0];
+    const int sub = lane % LPK, gi = lane / LPK;
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        /* l is replicated over the LPK lanes of a group */
-        const float lw = group_sum<64>(l[h]) * (1.0f / LPK);
-        if (lane == 0) {
-            s_m[wave][h] = m[h];
-            s_l[wave][h] = lw;
-        }
+        if (sub == 0) s_lg[h][wave * GPW + gi] = l[h];
+        if (lane == 0) s_m[wave][h] = m[h];
     }
     const bool single = (n_split == 1);
     const bool last_merges = p.counters != nullptr;
     const u32 pb = (grow * p.n_head + kvh * G) * n_split;
+    /* reader mapping: t -> (sub, part, k4, hh) */
+    const int rsub = tid % LPK, rpart = (tid / LPK) % TPC, rest = tid / (LPK * TPC);
+    const int rk4 = rest % 4, rhh = rest / 4;
 #pragma unroll
     for (int h0 = 0; h0 < G; h0 += HB) {
-        if (h0) __syncthreads();
+        if (h0) __syncthreads();                      /* previous round read */
+        float4 *mine = s_w4 + wave * WREG;
 #pragma unroll
         for (int hh = 0; hh < HB; hh++)
             if (h0 + hh < G)
 #pragma unroll
                 for (int k4 = 0; k4 < 4; k4++)
-                    s_acc4[(hh * 4 + k4) * NT + tid] =
+                    mine[(hh * 4 + k4) * 64 + lane] =
                         make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
                                     acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
         __syncthreads();
+        if (h0 == 0) TL_TRACE(2);
         if (h0 == 0) TL_TRACE(8);
-        const int col = tid / TPC, part = tid % TPC;
-        if (col < COLB && h0 + col / (D / 4) < G) {
-            const int hh = col / (D / 4), d = (col % (D / 4)) * 4;
-            const int h = h0 + hh;
-            const int csub = d / 16, k4 = (d % 16) / 4;
+        const int h = h0 + rhh;
+        if (rhh < HB && h < G) {
+            const int d = rsub * 16 + rk4 * 4;
             float mm = s_m[0][h];
 #pragma unroll
             for (int w = 1; w < W; w++) mm = fmaxf(mm, s_m[w][h]);
             const float mu = (mm == NEG_INF) ? 0.f : mm;
             float L = 0.f;
             float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 *src = s_acc4 + (hh * 4 + k4) * NT + csub;
+            const float4 *src = s_w4 + (rhh * 4 + rk4) * 64 + rsub;
 #pragma unroll
-            for (int i = 0; i < NLC / TPC; i++) {
-                const int li = part + i * TPC;               /* lane index among NLC */
-                const int w = li / (64 / LPK), gi = li % (64 / LPK);
+            for (int w = 0; w < W; w++) {
                 const float e = fast_exp2(s_m[w][h] - mu);
-                const float4 a = src[w * 64 + gi * LPK];
+                float lw = 0.f;
+                float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int g = 0; g < GPW; g += TPC) {
+                    const float4 t = src[w * WREG + (g + rpart) * LPK];
+                    lw += s_lg[h][w * GPW + g + rpart];
+                    a.x += t.x; a.y += t.y; a.z += t.z; a.w += t.w;
+                }
+                L = fmaf(e, lw, L);
                 O.x = fmaf(e, a.x, O.x);
                 O.y = fmaf(e, a.y, O.y);
                 O.z = fmaf(e, a.z, O.z);
                 O.w = fmaf(e, a.w, O.w);
             }
 #pragma unroll
-            for (int w = 0; w < W; w++) L += s_l[w][h] * fast_exp2(s_m[w][h] - mu);
-            O.x = group_sum<TPC>(O.x);
-            O.y = group_sum<TPC>(O.y);
-            O.z = group_sum<TPC>(O.z);
-            O.w = group_sum<TPC>(O.w);
-            if (part == 0) {
+            for (int x = LPK; x < LPK * TPC; x *= 2) {
+                L += __shfl_xor(L, x);
+                O.x += __shfl_xor(O.x, x);
+                O.y += __shfl_xor(O.y, x);
+                O.z += __shfl_xor(O.z, x);
+                O.w += __shfl_xor(O.w, x);
+            }
+            if (rpart == 0) {
                 const u32 hq = kvh * G + h;
                 if (single) {
                     const float inv = 1.0f / L;
@@ -1305,6 +766,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
      * Its partial stores are complete (vmcnt 0) before the counter add, so
      * the workgroup that sees n_split - 1 reads every partial. */
     __shared__ u32 s_last;
+    TL_TRACE(12);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     TL_TRACE(3);
@@ -1315,39 +777,31 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     if (s_last != n_split - 1) return;
     if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     TL_TRACE(9);
-    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq);
+    /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */
+    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0][0][0]);
 #ifdef TL_DEC_TRACE
     __syncthreads();
     TL_TRACE(4);
 #endif
 }
 
-/* One decode kernel instance: entry point and K (or V) bytes per wave tile
- * (the RoPE-fusing instances are separate so the plain ones carry none of
- * its code):
- * 4 KB (16 keys at head_dim 128).  Small tiles give each wave more pipeline
- * iterations per chunk and keep GQA groups of up to 8 heads within two waves
- * per SIMD (8 KB tiles measured slower: 35.1 vs 31.8 us at config 4). */
+/* One decode kernel instance: entry point, K (or V) bytes per wave tile and
+ * threads per workgroup.  The RoPE-fusing instances are separate so the
+ * plain ones carry none of its code. */
 struct DecKernel {
     const void *fn;
     int tile_bytes;
     int threads;
 };
 
-static u32 env_u32(const char *name, u32 dflt);
-
 template <int D>
 static DecKernel pick_kernel(int G, bool rope) {
-    const bool v1 = env_u32("TL_DECODE_V1", 0) != 0;
+    constexpr int NT = 64 * TL_RING_WAVES;
     switch (G) {
-#define TL_CASE(g)                                                                        \
-    case g:                                                                               \
-        if (!v1) {                                                                        \
-            if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true>, 4096, 64 * TL_RING_WAVES}; \
-            return {(const void *)attn_decode_ring_kernel<D, g, false>, 4096, 64 * TL_RING_WAVES};          \
-        }                                                                                 \
-        if (rope) return {(const void *)attn_decode_kernel<D, g, 4096, true>, 4096, 256}; \
-        return {(const void *)attn_decode_kernel<D, g, 4096, false>, 4096, 256};
+#define TL_CASE(g)                                                                       \
+    case g:                                                                              \
+        if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true>, 4096, NT};  \
+        return {(const void *)attn_decode_ring_kernel<D, g, false>, 4096, NT};
         TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
         TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
 #undef TL_CASE
