@@ -581,7 +581,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(),
-                     "kernel": "attn_decode_kernel<128,4,4096> (one OP_ATTN launch, "
+                     "kernel": "attn_decode_ring_kernel<128,4,false> (one OP_ATTN launch, "
                                "split merge inside)"},
     }
     if not args.no_prefill_attn:

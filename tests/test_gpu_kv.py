@@ -404,3 +404,46 @@ def test_prefill_split_invariance(T):
         outs.append(out)
     assert np.abs(outs[0] - outs[1]).max() < 1e-4
     assert np.abs(outs[0] - outs[2]).max() < 1e-4
+
+
+@pytest.mark.parametrize("case", [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted slots: GQA ratios the
+    # BASELINE shapes do not use, and the largest fused decode batch
+    (12, 4, 128, 2048, 1900, 1, 0, True),     # gqa 3
+    (20, 4, 128, 2048, 1900, 1, 0, False),    # gqa 5
+    (24, 4, 64, 2048, 1900, 1, 0, True),      # gqa 6, head_dim 64
+    (16, 2, 256, 2048, 1500, 2, 0, True),     # gqa 8, head_dim 256, 2 rows
+    (32, 8, 128, 4096, 3000, 15, 0, True),    # 15 new rows in one decode launch
+    (32, 8, 128, 4096, 3000, 15, 700, False), # same, windowed
+])
+def test_attn_more_shapes_vs_oracle(T, case):
+    n_head, n_kv, hd, cap, pos, n, window, perm = case
+    rng = np.random.default_rng(pos + n)
+    slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                    seed=pos + 3 * n)
+    assert np.abs(out - o16).max() < TOL
+    assert np.abs(out - o32).max() < TOL
+
+
+def test_decode_deterministic_across_launches(T):
+    """The same decode call repeated on the same cache gives bit-identical
+    outputs (fixed split boundaries and merge order)."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos = 32, 8, 128, 20000, 19000
+    rng = np.random.default_rng(21)
+    L = tlkv.Layer(cap, n_kv, hd)
+    kd = n_kv * hd
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, rows(rng, pos, kd))),
+                                       tlkv.ptr(dev(T, rows(rng, pos, kd))), kd, None, 0, pos,
+                                       None))
+    q = dev(T, rows(rng, 1, n_head * hd))
+    outs = []
+    for _ in range(3):
+        out = T.zeros((1, n_head * hd), dtype=T.float32, device="cuda")
+        a = tlkv.attn_args(q, None, None, out, None, pos, 1, n_head, hd, n_kv, 0,
+                           O.scale_of(hd))
+        tlkv.check(tlkv.lib().tl_attn_noappend(L.desc, a, None))
+        sync(T)
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
