@@ -7,28 +7,27 @@
  * n_keys > window (cpu_op.c:1019-1022); s_t = (K[h/gqa][slot_t] . q) * scale;
  * out = softmax(s) @ V.
  *
- * Work decomposition (gfx950, wave64):
- *   grid = n_split x (rows x n_kv_head) workgroups of 4 waves, two resident
- *   per CU, mapped so that all splits of one (row, kv-head) group run on one
- *   XCD.  A workgroup streams one contiguous chunk of keys of one kv-head and
- *   serves every q-head of the GQA group from the same K/V bytes, so each
- *   cache byte is read from HBM once per step instead of gqa times.  The
- *   chunk's slot indices are staged in LDS first, so K/V loads never wait on
- *   a dependent slot-table load.
- *   Each wave owns every 4th tile of the chunk (4 KB of K+V by default):
- *   16-byte loads into registers, written to a per-wave LDS tile (K chunks
- *   XOR-swizzled by row against bank conflicts) while the next tile's loads
- *   are in flight.
+ * Work decomposition (gfx950, wave64): attn_decode_ring_kernel.
+ *   grid = n_split x (rows x n_kv_head) workgroups of 8 waves, one per CU,
+ *   mapped so that all splits of one (row, kv-head) group run on one XCD.  A
+ *   workgroup streams one contiguous chunk of keys of one kv-head and serves
+ *   every q-head of the GQA group from the same K/V bytes, so each cache byte
+ *   is read from HBM once per step instead of gqa times.  The chunk's slot
+ *   indices and q are staged in LDS first.
+ *   Each wave owns every 8th tile (4 KB of K + 4 KB of V) and streams it
+ *   through a 2-stage LDS ring filled by non-temporal LDS-direct loads.
  *   Scores: v_dot2_f32_f16 of the f16 K row with q (pre-scaled by
- *   scale*log2(e), rounded to f16), summed over the row's lanes with DPP
- *   moves; wave-uniform online softmax per q-head in f32 with exp2; p is
- *   rounded to f16 and PV runs as v_dot2 over key pairs of V.
+ *   scale*log2(e), rounded to f16), reduced over the key's lanes with DPP;
+ *   each lane group keeps its own (l, acc) against a wave-uniform running
+ *   max that moves only when a score exceeds it by 2^8; p is rounded to f16
+ *   and PV runs as v_dot2 over key pairs of V.
  *   States merge across waves through LDS and across splits in the last
  *   workgroup of the group to finish (partials written with device-coherent
  *   stores, a per-group atomic counter that this workgroup resets), or in a
  *   separate merge launch when the partials exceed that workgroup's LDS.
- *   The fused append of decode rows: the split-0 workgroup writes the new
- *   K/V rows; workgroups that need a new key convert it from the f32 input.
+ *   The fused append of decode rows: the split-0 workgroup of row 0 writes
+ *   the new K/V rows; workgroups that need a new key convert it from the f32
+ *   input into LDS.
  */
 #include "tl_common.h"
 #include "tl_internal.h"
@@ -406,7 +405,7 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
  * LPK lanes keeps its own online-softmax state (no cross-lane exchange in
  * the stream loop); the groups and waves merge once at the end.  Split
  * decomposition, XCD-aware block order, GQA sharing, the fused append and
- * the split merge are those of attn_decode_kernel.  Tiles that hold rows
+ * the split merge are described at the top of this file.  Tiles that hold rows
  * appended by this launch (the last tiles of the last split) are filled
  * from registers after the ring has drained. */
 #define TL_RING_WAVES 8

@@ -7,13 +7,10 @@
  *   kv_gather_kernel    read rows by slot.
  *   kv_copy_kernel      row copies across all layers (fork / compaction).
  *   rope_kernel         OP_ROPE_NORM / OP_ROPE_NEOX (cpu_op.c:632-700).
- *   attn_decode_kernel  split-K ("flash-decoding") attention over the slot
- *                       table, one workgroup per (split, kv-head, row) serving
- *                       all q-heads of the GQA group; scores and softmax in
- *                       f32 with per-lane-group online softmax, wave merges
- *                       through DPP/shuffles, workgroup merge through LDS and
- *                       a last-workgroup LSE merge of the splits.
- *                       Math of cpu_op.c:1011-1062.
+ *   The decode attention (tl_decode.hip, attn_decode_ring_kernel) is
+ *   split-K ("flash-decoding") attention over the slot table, one workgroup
+ *   per (split, kv-head, row) serving all q-heads of the GQA group; math of
+ *   cpu_op.c:1011-1062.
  * The MFMA chunked-prefill kernel lives in tl_prefill.hip.
  */
 #include "tl_common.h"
