@@ -102,85 +102,62 @@ extern "C" int tl_dec_trace_read(void *host, size_t bytes) {
 #define TL_TRACE_IDS() do {} while (0)
 #endif
 
-/* Split merge as its own launch (no cross-workgroup synchronisation inside
- * the decode kernel).  grid = rows * n_head, 256 threads.  Weights
- * w_s = exp2(m_s - M) go to LDS; the n_split partial rows are then summed by
- * 256/D thread subsets with independent loads, and the subsets are added. */
+/* Split merge as its own launch (prefill key splits, and decode splits whose
+ * partials exceed the in-launch merge).  D/4 threads per output row of one
+ * head, each owning a float4: it folds the n_split partials of its float4
+ * with an online max, in batches of 8 (all loads of a batch requested
+ * together): out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s.
+ * grid = ceil(rows * n_head * D/4 / 256), no LDS, no barriers. */
 #define TL_MERGE_MAX_SPLIT 1024
 template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p, u32 n_out) {
     constexpr float NEG_INF = -__builtin_huge_valf();
-    constexpr int SUB = 256 / D;      /* thread subsets over the splits */
-    constexpr int B = 16;             /* partial rows in flight per thread */
-    __shared__ float s_m[TL_MERGE_MAX_SPLIT];
-    __shared__ float s_lw[TL_MERGE_MAX_SPLIT];
-    __shared__ float s_red[8];
-    __shared__ float s_part[SUB][D];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const u32 hq = blockIdx.x % p.n_head;
-    const u32 grow = blockIdx.x / p.n_head;
+    constexpr int C4 = D / 4;
+    constexpr int K = 8;
+    const u32 gid = blockIdx.x * 256 + threadIdx.x;
+    const u32 o = gid / C4;                       /* (row, head) */
+    if (o >= n_out) return;
+    const u32 d = (gid % C4) * 4;
+    const u32 hq = o % p.n_head, grow = o / p.n_head;
     const u32 si = grow / p.rows_per_seq, r = grow % p.rows_per_seq;
     const u32 ns = p.n_split;
-    const u64 pb = ((u64)grow * p.n_head + hq) * ns;
-    const int d = tid % D, sub = tid / D;
-    const float *src = p.ws_acc + pb * D + d;
-
-    /* one round trip: split maxima/sums and the first B partial elements */
-    float a[B];
+    const u64 pb = (u64)o * ns;
+    float M = NEG_INF, L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (u32 s0 = 0; s0 < ns; s0 += K) {
+        float2 ml[K];
+        float4 a[K];
 #pragma unroll
-    for (int k = 0; k < B; k++) {
-        const u32 s = sub + k * SUB;
-        a[k] = s < ns ? src[(u64)s * D] : 0.f;
-    }
-    float mm = NEG_INF;
-    for (u32 s = tid; s < ns; s += 256) {
-        const float2 ml = p.ws_ml[pb + s];
-        s_m[s] = ml.x;
-        s_lw[s] = ml.y;
-        mm = fmaxf(mm, ml.x);
-    }
-    mm = group_max<64>(mm);
-    if (lane == 0) s_red[wave] = mm;
-    __syncthreads();
-    mm = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float mu = (mm == NEG_INF) ? 0.f : mm;
-    float L = 0.f;
-    for (u32 s = tid; s < ns; s += 256) {
-        const float w = fast_exp2(s_m[s] - mu);
-        s_m[s] = w;
-        L += w * s_lw[s];
-    }
-    L = group_sum<64>(L);
-    if (lane == 0) s_red[4 + wave] = L;
-    __syncthreads();
-    L = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
-
-    float O = 0.f;
-#pragma unroll
-    for (int k = 0; k < B; k++) {
-        const u32 s = sub + k * SUB;
-        if (s < ns) O = fmaf(s_m[s], a[k], O);
-    }
-    for (u32 s0 = B * SUB; s0 < ns; s0 += B * SUB) {   /* more than B*SUB splits */
-#pragma unroll
-        for (int k = 0; k < B; k++) {
-            const u32 s = s0 + sub + k * SUB;
-            a[k] = s < ns ? src[(u64)s * D] : 0.f;
+        for (int k = 0; k < K; k++) {
+            const u32 s = min(s0 + k, ns - 1);
+            ml[k] = p.ws_ml[pb + s];
+            a[k] = *(const float4 *)&p.ws_acc[(pb + s) * D + d];
         }
+        float bm = NEG_INF;
 #pragma unroll
-        for (int k = 0; k < B; k++) {
-            const u32 s = s0 + sub + k * SUB;
-            if (s < ns) O = fmaf(s_m[s], a[k], O);
+        for (int k = 0; k < K; k++) {
+            if (s0 + k >= ns) ml[k] = make_float2(NEG_INF, 0.f);
+            bm = fmaxf(bm, ml[k].x);
+        }
+        const float nm = fmaxf(M, bm);
+        const float mu = (nm == NEG_INF) ? 0.f : nm;
+        const float sc = fast_exp2(M - mu);
+        L *= sc;
+        O.x *= sc; O.y *= sc; O.z *= sc; O.w *= sc;
+        M = nm;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const float w = fast_exp2(ml[k].x - mu);
+            L = fmaf(w, ml[k].y, L);
+            O.x = fmaf(w, a[k].x, O.x);
+            O.y = fmaf(w, a[k].y, O.y);
+            O.z = fmaf(w, a[k].z, O.z);
+            O.w = fmaf(w, a[k].w, O.w);
         }
     }
-    s_part[sub][d] = O;
-    __syncthreads();
-    if (tid < D) {
-        float o = 0.f;
-#pragma unroll
-        for (int k = 0; k < SUB; k++) o += s_part[k][tid];
-        p.seq[si].dst[(u64)r * p.q_stride + (u64)hq * D + tid] = o / L;
-    }
+    const float inv = 1.0f / L;
+    *(float4 *)&p.seq[si].dst[(u64)r * p.q_stride + (u64)hq * D + d] =
+        make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -899,11 +876,12 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
 
 int tl_launch_merge(const DecParams &p, u32 n_rows_total, u32 head_dim, hipStream_t st) {
     if (p.n_split > TL_MERGE_MAX_SPLIT) return tl_fail(TL_EINVAL, "merge: %u splits", p.n_split);
-    dim3 mg(n_rows_total * p.n_head);
+    const u32 n_out = n_rows_total * p.n_head;
+    const dim3 mg((u32)(((u64)n_out * (head_dim / 4) + 255) / 256));
     switch (head_dim) {
-    case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(256), 0, st, p); break;
-    case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(256), 0, st, p); break;
-    case 256: hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(256), 0, st, p); break;
+    case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(256), 0, st, p, n_out); break;
+    case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(256), 0, st, p, n_out); break;
+    case 256: hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(256), 0, st, p, n_out); break;
     default: return tl_fail(TL_EINVAL, "merge: head_dim %u", head_dim);
     }
     HIP_TRY(hipGetLastError());
