@@ -511,6 +511,36 @@ def main():
     bytes_total = sum(L * decode_bytes(c, pos0 + s + 1) for s in range(K))
     value = bytes_total / (total_ms / 1e3) / 1e9
 
+    # the same decode over the contiguous cache (no slot table: the layout the
+    # reference's device backend uses, graph.c:860-870 builds the radix map
+    # only for CPU layers); the slots above are the identity, so the rows are
+    # the same
+    cont_steps = min(128, K)
+    args_c = [tlkv.attn_args(q[l], None, None, out[l], None, pos - 1, 1, Hq, d, Hkv, 0, scale)
+              for l in range(L)]
+    noapp = lib.tl_attn_noappend
+    for l in range(L):
+        tlkv.check(noapp(descs[l], args_c[l], sh))
+    torch.cuda.synchronize()
+    c0, c1 = ev(), ev()
+    c0.record(stream)
+    for _ in range(cont_steps):
+        for l in range(L):
+            rc = noapp(descs[l], args_c[l], sh)
+            if rc:
+                tlkv.check(rc)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    cont_us = c0.elapsed_time(c1) * 1e3 / (cont_steps * L)
+    cont_bytes = decode_bytes(c, pos) - Hkv * d * 2 * 6     # no appended row
+    decode_contiguous = {"us_per_layer_launch": round(cont_us, 3),
+                         "GBs": round(cont_bytes / (cont_us * 1e-6) / 1e9, 1),
+                         "hbm_frac": round(cont_bytes / (cont_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "steps": cont_steps,
+                         "note": "OP_ATTN without the slot table (contiguous cache, the "
+                                 "reference's device layout) and without the fused append, "
+                                 f"P = {pos} keys"}
+
     # decode step with RoPE on q and the new k row (the reference's OP_ROPE x2
     # + OP_ATTN): three launches per layer (tl_rope, tl_rope, tl_attn) vs one
     # (tl_attn_rope), on raw (un-rotated) q/k rows; cache rows written past
@@ -571,6 +601,7 @@ def main():
         "decode": {"us_per_layer_launch": round(avg_launch_us, 3),
                    "tok_s": round(K / (total_ms / 1e3), 1),
                    "frac_of_measured_ceiling": round(value / ceiling, 4)},
+        "decode_contiguous": decode_contiguous,
         "decode_with_rope_us_per_layer": {**rope_us, "steps": rope_steps,
                                           "note": "RoPE on q and the new k row each step: "
                                                   "tl_rope x2 + tl_attn vs tl_attn_rope"},
