@@ -185,6 +185,55 @@ int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t heads,
             uint32_t head_dim, uint32_t rope_dim, uint32_t pos, float theta,
             int neox, void *stream);
 
+/* ---- Q8_0 cache ------------------------------------------------------------
+ * A quantized KV cache (the reference's cache is f32, and its notes list a
+ * quantized KV cache as missing, REMEMBER.md:18).  Each row of each head is
+ * cut into blocks of 32 elements stored in the GGUF Q8_0 form the reference
+ * dequantizes (src/quants.c:368-373: value = q * d, q int8, d binary16),
+ * with the values and the scales in two planes so every row stays 16-byte
+ * aligned:
+ *   k, v    int8 [n_kv_head][cap][head_dim]
+ *   ks, vs  f16  [n_kv_head][cap][head_dim / 32]
+ * Quantization of a block x[32] is the reference's Q8_0 quantizer
+ * (src/backend/gpu/gpu.cu:1077-1086): amax = max |x_j|, d = amax / 127,
+ * q_j = rint(x_j * (d > 0 ? 1/d : 0)) (ties to even), d stored RNE as
+ * binary16.  Inputs are expected finite.  Attention over a Q8_0 cache
+ * equals attention over the dequantized values q * d.  No counterpart in
+ * the reference's KV API (an added format); RoPE is not fused on this path
+ * (apply tl_rope to q and k first). */
+typedef struct tl_kv_layer_q8 {
+    void     *k;          /* device, int8 [n_kv_head][cap][head_dim] */
+    void     *v;
+    void     *ks;         /* device, f16 [n_kv_head][cap][head_dim/32] */
+    void     *vs;
+    uint32_t  cap;
+    uint32_t  n_kv_head;
+    uint32_t  head_dim;   /* 64, 128 or 256 */
+    uint32_t  ring;       /* as tl_kv_layer.ring */
+} tl_kv_layer_q8;
+
+int tl_kv_layer_alloc_q8(tl_kv_layer_q8 *L, uint32_t cap, uint32_t n_kv_head,
+                         uint32_t head_dim, uint32_t ring);
+int tl_kv_layer_free_q8(tl_kv_layer_q8 *L);
+
+/* Quantize and write n rows of K and V at slots[pos+i] (as tl_kv_append). */
+int tl_kv_append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v,
+                    uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                    uint32_t n, void *stream);
+
+/* Read rows slots[i] of every head: values to k_out/v_out
+ * [n][n_kv_head][head_dim] int8, scales to ks_out/vs_out
+ * [n][n_kv_head][head_dim/32] f16 bits (device). */
+int tl_kv_gather_q8(const tl_kv_layer_q8 *L, const uint32_t *slots, uint32_t n,
+                    int8_t *k_out, uint16_t *ks_out, int8_t *v_out, uint16_t *vs_out,
+                    void *stream);
+
+/* OP_ATTN over a Q8_0 cache: quantize-append the batch rows, then attend
+ * (decode-sized batches: the split-K kernel reading the int8 rows; larger
+ * ones: the MFMA kernel, which dequantizes its K/V tiles to f16 in LDS). */
+int tl_attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *stream);
+int tl_attn_noappend_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *stream);
+
 /* Measurement aid (no reference counterpart): stream `bytes` of device
  * memory with 16-byte loads, `depth` (1/4/8/16) in flight per lane, over
  * `blocks` workgroups of 256; sink receives blocks*256 words.  Gives the

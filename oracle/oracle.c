@@ -20,6 +20,17 @@
  *                      sliding-window rule :1019-1022 and softmax :338-349.
  *                      Pinned against the compiled reference (cpu_graph_op)
  *                      through committed golden vectors, plus closed forms.
+ *   or_q8_quantize     one 32-element Q8_0 block, the reference's quantizer
+ *                      src/backend/gpu/gpu.cu:1077-1086 (amax, d = amax/127,
+ *                      id = d > 0 ? 1/d : 0, q = rint(x*id)), with d kept as
+ *                      binary16 as the GGUF Q8_0 block stores it.  Pinned by
+ *                      tests on constructed blocks (ties to even, the amax
+ *                      element -> +-127, zero blocks, error <= d/2).
+ *   or_q8_dequant      quants.c:368-373 (value = q * f16_to_f32(d)).  Pinned
+ *                      against the compiled reference's gguf_dequant.
+ *   or_kv_append_q8 /  the write-through and op_attn over a Q8_0 cache: the
+ *   or_attn_q8         rows are quantized on write; attention reads the
+ *                      dequantized values (same loop as or_attn).
  *   or_rope_norm/neox  op_rope_norm cpu_op.c:674-700, rope_partial/op_rope_neox
  *                      cpu_op.c:632-670 (f32 libm powf/cosf/sinf).  Pinned by
  *                      golden vectors from the compiled reference, within
@@ -169,40 +180,37 @@ static void h2f_init(void) {
     g_h2f_ready = 1;
 }
 
-/* one cached row as f32 */
-static inline const float *cache_row(const void *c, int f16, u64 off, u32 khd, float *tmp) {
-    if (!f16) return (const float *)c + off;
-    const u16 *h = (const u16 *)c + off;
-    for (u32 d = 0; d < khd; d++) tmp[d] = g_h2f[h[d]];
+/* A layer cache as the attention loop reads it: f32, f16, or Q8_0 (int8
+ * values plus one binary16 scale per 32 elements, planar). */
+typedef struct {
+    int type;                      /* 0 f32, 1 f16, 2 q8_0 */
+    const void *k, *v;
+    const u16 *ks, *vs;
+    u32 cap, khd;
+} CacheView;
+
+/* one cached row (kv-head h, physical row slot) of K (which 0) or V as f32 */
+static const float *view_row(const CacheView *c, int which, u32 h, u32 slot, float *tmp) {
+    u64 off = ((u64)h * c->cap + slot) * c->khd;
+    const void *base = which ? c->v : c->k;
+    if (c->type == 0) return (const float *)base + off;
+    if (c->type == 1) {
+        const u16 *x = (const u16 *)base + off;
+        for (u32 d = 0; d < c->khd; d++) tmp[d] = g_h2f[x[d]];
+        return tmp;
+    }
+    const int8_t *x = (const int8_t *)base + off;
+    const u16 *sc = (which ? c->vs : c->ks) + off / 32;
+    for (u32 d = 0; d < c->khd; d++) tmp[d] = (float)x[d] * g_h2f[sc[d / 32]];
     return tmp;
 }
 
-/* op_attn restated: write the batch's K/V rows (converted to the cache
- * type), then for every q-head h and batch row qi attend over the visible
- * keys start..pos+qi through the slot table.  dst [n][n_head*hd] f32.
- * ring != 0 selects the ring layout for windowed layers: the physical row
- * of logical position p is p % ring (slots ignored); it is only valid when
- * ring >= win + n - 1 so no row still visible to this batch is overwritten. */
-int or_attn(const float *q, const float *k, const float *v, float *dst,
-            void *kc, void *vc, int cache_f16, u32 cap, u32 ring,
-            const u32 *slots, u32 pos, u32 n,
-            u32 n_head, u32 n_kv, u32 hd, u32 khd, u32 win, float scale) {
-    u32 q_dim = n_head * hd, kv_dim = n_kv * khd;
-    u32 gqa = n_head / n_kv;
-    u64 hs = (u64)cap * khd;
-    if (ring) {
-        if (ring > cap || (win && ring < win + n - 1) || !win) return -1;
-        for (u32 i = 0; i < n; i++) {
-            u32 slot = (pos + i) % ring;
-            int rc = or_kv_append(kc, vc, cache_f16, cap, n_kv, khd,
-                                  k + (u64)i * kv_dim, v + (u64)i * kv_dim, kv_dim,
-                                  NULL, slot, 1);
-            if (rc) return rc;
-        }
-    } else if (or_kv_append(kc, vc, cache_f16, cap, n_kv, khd, k, v, kv_dim,
-                            slots, pos, n)) {
-        return -1;
-    }
+/* attention of the batch over a cache that already holds its rows
+ * (cpu_op.c:1011-1062) */
+static int attn_rows(const float *q, float *dst, const CacheView *c, u32 ring,
+                     const u32 *slots, u32 pos, u32 n, u32 n_head, u32 n_kv, u32 hd,
+                     u32 win, float scale) {
+    u32 khd = c->khd, q_dim = n_head * hd, gqa = n_head / n_kv;
     h2f_init();
     float *scr = (float *)malloc(((size_t)pos + n) * sizeof(float));
     float *row = (float *)malloc((size_t)khd * sizeof(float));
@@ -222,12 +230,12 @@ int or_attn(const float *q, const float *k, const float *v, float *dst,
             for (u32 t = 0; t < n_vis; t++) {
                 u32 lp = start + t;
                 u32 slot = ring ? lp % ring : (slots ? slots[lp] : lp);
-                if (slot >= cap) {
+                if (slot >= c->cap) {
                     free(scr);
                     free(row);
                     return -1;
                 }
-                const float *kr = cache_row(kc, cache_f16, (u64)kv_h * hs + (u64)slot * khd, khd, row);
+                const float *kr = view_row(c, 0, kv_h, slot, row);
                 float sum = 0.0f;
                 for (u32 d = 0; d < khd; d++) sum += kr[d] * qh[d];
                 scr[t] = sum * scale;
@@ -237,7 +245,7 @@ int or_attn(const float *q, const float *k, const float *v, float *dst,
             for (u32 t = 0; t < n_vis; t++) {
                 u32 lp = start + t;
                 u32 slot = ring ? lp % ring : (slots ? slots[lp] : lp);
-                const float *vr = cache_row(vc, cache_f16, (u64)kv_h * hs + (u64)slot * khd, khd, row);
+                const float *vr = view_row(c, 1, kv_h, slot, row);
                 float st = scr[t];
                 for (u32 d = 0; d < khd; d++) oh[d] += st * vr[d];
             }
@@ -246,6 +254,95 @@ int or_attn(const float *q, const float *k, const float *v, float *dst,
     free(scr);
     free(row);
     return 0;
+}
+
+/* op_attn restated: write the batch's K/V rows (converted to the cache
+ * type), then for every q-head h and batch row qi attend over the visible
+ * keys start..pos+qi through the slot table.  dst [n][n_head*hd] f32.
+ * ring != 0 selects the ring layout for windowed layers: the physical row
+ * of logical position p is p % ring (slots ignored); it is only valid when
+ * ring >= win + n - 1 so no row still visible to this batch is overwritten. */
+int or_attn(const float *q, const float *k, const float *v, float *dst,
+            void *kc, void *vc, int cache_f16, u32 cap, u32 ring,
+            const u32 *slots, u32 pos, u32 n,
+            u32 n_head, u32 n_kv, u32 hd, u32 khd, u32 win, float scale) {
+    u32 kv_dim = n_kv * khd;
+    if (ring) {
+        if (ring > cap || (win && ring < win + n - 1) || !win) return -1;
+        for (u32 i = 0; i < n; i++) {
+            u32 slot = (pos + i) % ring;
+            int rc = or_kv_append(kc, vc, cache_f16, cap, n_kv, khd,
+                                  k + (u64)i * kv_dim, v + (u64)i * kv_dim, kv_dim,
+                                  NULL, slot, 1);
+            if (rc) return rc;
+        }
+    } else if (or_kv_append(kc, vc, cache_f16, cap, n_kv, khd, k, v, kv_dim,
+                            slots, pos, n)) {
+        return -1;
+    }
+    CacheView c = {cache_f16 ? 1 : 0, kc, vc, NULL, NULL, cap, khd};
+    return attn_rows(q, dst, &c, ring, slots, pos, n, n_head, n_kv, hd, win, scale);
+}
+
+/* ---- Q8_0 cache ----------------------------------------------------------- */
+
+/* Quantize one block of 32 (gpu.cu:1077-1086): amax = max |x|,
+ * d = amax / 127 (f32), id = d > 0 ? 1/d : 0, q = rint(x * id) in the
+ * default round-to-nearest-even mode (__float2int_rn); the stored scale is
+ * binary16(d), RNE, as the GGUF Q8_0 block holds it (quants.c:370-372). */
+void or_q8_quantize(const float *x, int8_t *q, u16 *d_out) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+    float d = amax / 127.0f;
+    float id = d > 0.0f ? 1.0f / d : 0.0f;
+    for (int j = 0; j < 32; j++) q[j] = (int8_t)(int)rintf(x[j] * id);
+    *d_out = or_f32_to_f16(d);
+}
+
+void or_q8_quantize_n(const float *x, u64 nblk, int8_t *q, u16 *d) {
+    for (u64 b = 0; b < nblk; b++) or_q8_quantize(x + 32 * b, q + 32 * b, d + b);
+}
+
+/* n elements of Q8_0 data (planar: q[n], d[n/32]) -> f32 (quants.c:368-373) */
+void or_q8_dequant(const int8_t *q, const u16 *d, u64 n, float *out) {
+    for (u64 i = 0; i < n; i++) out[i] = (float)q[i] * or_f16_to_f32(d[i >> 5]);
+}
+
+/* write-through into a Q8_0 cache: k8/v8 int8 [n_kv][cap][khd], ks/vs f16
+ * [n_kv][cap][khd/32]; slot rule of or_kv_append (ring: p % ring). */
+int or_kv_append_q8(int8_t *k8, u16 *ks, int8_t *v8, u16 *vs, u32 cap, u32 ring,
+                    u32 n_kv, u32 khd, const float *k, const float *v, u32 kv_dim,
+                    const u32 *slots, u32 pos, u32 n) {
+    if (khd % 32) return -1;
+    for (u32 i = 0; i < n; i++) {
+        u32 lp = pos + i;
+        u32 slot = ring ? lp % ring : (slots ? slots[lp] : lp);
+        if (slot >= cap) return -1;
+        for (u32 h = 0; h < n_kv; h++) {
+            u64 off = ((u64)h * cap + slot) * khd;
+            const float *kr = k + (u64)i * kv_dim + (u64)h * khd;
+            const float *vr = v + (u64)i * kv_dim + (u64)h * khd;
+            for (u32 b = 0; b < khd / 32; b++) {
+                or_q8_quantize(kr + 32 * b, k8 + off + 32 * b, ks + off / 32 + b);
+                or_q8_quantize(vr + 32 * b, v8 + off + 32 * b, vs + off / 32 + b);
+            }
+        }
+    }
+    return 0;
+}
+
+/* op_attn over a Q8_0 cache: quantize-append the batch rows (when k != NULL),
+ * then attend over the dequantized cache. */
+int or_attn_q8(const float *q, const float *k, const float *v, float *dst,
+               int8_t *k8, u16 *ks, int8_t *v8, u16 *vs, u32 cap, u32 ring,
+               const u32 *slots, u32 pos, u32 n, u32 n_head, u32 n_kv, u32 khd,
+               u32 win, float scale) {
+    if (ring && (ring > cap || !win || ring < win + n - 1)) return -1;
+    if (k && or_kv_append_q8(k8, ks, v8, vs, cap, ring, n_kv, khd, k, v, n_kv * khd,
+                             slots, pos, n))
+        return -1;
+    CacheView c = {2, k8, v8, ks, vs, cap, khd};
+    return attn_rows(q, dst, &c, ring, slots, pos, n, n_head, n_kv, khd, win, scale);
 }
 
 /* ---- RoPE (cpu_op.c:632-700) -------------------------------------------- */

@@ -53,6 +53,16 @@ def lib():
                               _u32, _u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                               _u32, ctypes.c_float]
         L.or_attn.restype = ctypes.c_int
+        _i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+        L.or_q8_quantize.argtypes = [_f32p, _i8p, _u16p]
+        L.or_q8_quantize_n.argtypes = [_f32p, ctypes.c_uint64, _i8p, _u16p]
+        L.or_q8_dequant.argtypes = [_i8p, _u16p, ctypes.c_uint64, _f32p]
+        L.or_kv_append_q8.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                      _f32p, _f32p, _u32, _vp, _u32, _u32]
+        L.or_kv_append_q8.restype = ctypes.c_int
+        L.or_attn_q8.argtypes = [_f32p, _vp, _vp, _f32p, _vp, _vp, _vp, _vp, _u32, _u32,
+                                 _vp, _u32, _u32, _u32, _u32, _u32, _u32, ctypes.c_float]
+        L.or_attn_q8.restype = ctypes.c_int
         for nm in ("or_rope_norm", "or_rope_neox"):
             getattr(L, nm).argtypes = [_f32p, _u32, _u32, _u32, _u32, _u32, _u32,
                                        ctypes.c_float]
@@ -86,6 +96,7 @@ def ref():
         R.rh_kv_slots.argtypes = [_vp, _u32p, _u32]
         R.rh_kv_stats.argtypes = [_vp, _u64p]
         R.rh_kv_meta.argtypes = [_vp, _u32, _u32p]
+        R.rh_dequant_q8_0.argtypes = [_vp, ctypes.c_uint64, _f32p]
         _ref = R
     return _ref
 
@@ -163,6 +174,68 @@ def attn(cache, q, k, v, slots, pos, n, n_head, window=0, ring=0, scale=None):
     return dst.reshape(n, n_head * khd)
 
 
+# ---- Q8_0 ---------------------------------------------------------------------
+
+def q8_quantize(x):
+    """f32 [..., 32k] -> (int8 values, f16 scale bits [..., k]) (oracle.c or_q8_quantize)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    blocks = x.reshape(-1, 32)
+    q = np.empty(blocks.shape, dtype=np.int8)
+    d = np.empty(blocks.shape[0], dtype=np.uint16)
+    lib().or_q8_quantize_n(blocks.reshape(-1), blocks.shape[0], q.reshape(-1), d)
+    return q.reshape(x.shape), d.reshape(x.shape[:-1] + (x.shape[-1] // 32,))
+
+
+def q8_dequant(q, d):
+    """planar Q8_0 (int8 values, f16 scale bits) -> f32 (quants.c:368-373)."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    d = np.ascontiguousarray(d, dtype=np.uint16)
+    out = np.empty(q.shape, dtype=np.float32)
+    lib().or_q8_dequant(q.reshape(-1), d.reshape(-1), q.size, out.reshape(-1))
+    return out
+
+
+class CacheQ8:
+    """One layer's Q8_0 cache: int8 [n_kv][cap][khd] + f16 scales [n_kv][cap][khd/32]."""
+
+    def __init__(self, cap, n_kv, khd, ring=0):
+        self.k = np.zeros((n_kv, cap, khd), dtype=np.int8)
+        self.v = np.zeros_like(self.k)
+        self.ks = np.zeros((n_kv, cap, khd // 32), dtype=np.uint16)
+        self.vs = np.zeros_like(self.ks)
+        self.cap, self.n_kv, self.khd, self.ring = cap, n_kv, khd, ring
+
+    def _ptrs(self):
+        return (self.k.ctypes.data, self.ks.ctypes.data, self.v.ctypes.data,
+                self.vs.ctypes.data)
+
+    def append(self, k, v, slots, pos, n):
+        k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.uint32)
+        return lib().or_kv_append_q8(*self._ptrs(), self.cap, self.ring, self.n_kv, self.khd,
+                                     k, v, self.n_kv * self.khd,
+                                     None if sl is None else sl.ctypes.data, pos, n)
+
+    def attn(self, q, k, v, slots, pos, n, n_head, window=0, scale=None):
+        """op_attn over this cache (k None: rows already appended)."""
+        khd = self.khd
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+        if k is not None:
+            k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
+            v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        dst = np.zeros(n * n_head * khd, dtype=np.float32)
+        sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.uint32)
+        rc = lib().or_attn_q8(q, None if k is None else k.ctypes.data,
+                              None if v is None else v.ctypes.data, dst, *self._ptrs(),
+                              self.cap, self.ring, None if sl is None else sl.ctypes.data,
+                              pos, n, n_head, self.n_kv, khd, window,
+                              scale_of(khd) if scale is None else scale)
+        if rc:
+            raise ValueError(f"or_attn_q8 failed ({rc})")
+        return dst.reshape(n, n_head * khd)
+
+
 def rope(x, heads, hdim, rdim, pos, theta, neox):
     x = np.ascontiguousarray(x, dtype=np.float32).copy()
     rows, stride = x.shape
@@ -199,6 +272,15 @@ def ref_rope(x, heads, hdim, rdim, pos, theta, neox):
                        hdim, rdim, pos, theta)
     if rc:
         raise ValueError("reference rope returned false")
+    return out
+
+
+def ref_dequant_q8_0(blocks):
+    """GGUF Q8_0 blocks uint8 [nblk][34] -> f32 [nblk*32] via the reference."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n = blocks.shape[0] * 32
+    out = np.empty(n, dtype=np.float32)
+    ref().rh_dequant_q8_0(blocks.ctypes.data, n, out)
     return out
 
 

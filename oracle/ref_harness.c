@@ -7,6 +7,7 @@
  *   rh_attn      -> cpu_graph_op(OP_ATTN)      src/backend/cpu/cpu_op.c:1070,964
  *   rh_rope      -> cpu_graph_op(OP_ROPE_*)    src/backend/cpu/cpu_op.c:653,674
  *   rh_kv_*      -> kv_cache_create/match/append/destroy  src/kvcache.c:122-270
+ *   rh_dequant_q8_0 -> gguf_dequant(GGUF_TYPE_Q8_0)  src/quants.c:640-652,368
  *
  * The structs are the reference's own (def.h / kvcache.h); only the fields
  * op_attn reads are populated (cpu_op.c:968-993).
@@ -17,6 +18,7 @@
 #include "def.h"
 #include "kvcache.h"
 #include "backend/cpu/cpu_op.h"
+#include "quants.h"
 
 /* --- attention ----------------------------------------------------------- */
 
@@ -77,6 +79,19 @@ int rh_attn(const float *q, const float *k, const float *v, float *dst,
     free(scr);
     free(s);
     return ok ? 0 : -1;
+}
+
+/* --- Q8_0 dequant ---------------------------------------------------------- */
+
+/* n elements of GGUF Q8_0 blocks (34 bytes: f16 d, 32 x int8) -> f32,
+ * element by element through the reference's dispatcher. */
+void rh_dequant_q8_0(const u8 *blocks, u64 n, float *out) {
+    TensorInfo ti;
+    memset(&ti, 0, sizeof(ti));
+    ti.type = GGUF_TYPE_Q8_0;
+    ti.data = (void *)blocks;
+    ti.n_element = n;
+    for (u64 i = 0; i < n; i++) out[i] = gguf_dequant(&ti, i);
 }
 
 /* --- RoPE ---------------------------------------------------------------- */

@@ -12,6 +12,9 @@ Fixtures (numpy .npz, no pickles):
   op_attn.npz        cpu_graph_op(OP_ATTN) outputs over an f32 cache for tiny
                      GQA / window / slot-table cases (inputs included).
   rope.npz           cpu_graph_op(OP_ROPE_NORM / OP_ROPE_NEOX) outputs.
+  q8_0_dequant.npz   gguf_dequant(GGUF_TYPE_Q8_0) over GGUF Q8_0 blocks with
+                     random int8 values (all 256 codes) and binary16 scales
+                     (normal, subnormal, zero, negative).
 """
 import os
 import sys
@@ -138,6 +141,22 @@ def gen_rope():
     np.savez_compressed(os.path.join(HERE, "rope.npz"), **arrays)
 
 
+def gen_q8():
+    rng = np.random.default_rng(3000)
+    nblk = 96
+    q = rng.integers(-128, 128, size=(nblk, 32)).astype(np.int8)
+    q[0] = np.arange(-128, -96, dtype=np.int8)       # every code appears
+    q[1:8] = np.arange(-96, 128, dtype=np.int16).reshape(7, 32).astype(np.int8)
+    d = O.f16_bits(rng.uniform(1e-3, 2.0, size=nblk).astype(np.float32))
+    d[8:12] = [0x0000, 0x8000, 0x0001, 0x03ff]       # zeros and subnormals
+    d[12:16] = O.f16_bits(np.array([-0.5, 65504.0, 6.1035e-05, 1.0], dtype=np.float32))
+    blocks = np.zeros((nblk, 34), dtype=np.uint8)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nblk, 2)
+    blocks[:, 2:] = q.view(np.uint8)
+    out = O.ref_dequant_q8_0(blocks)
+    np.savez_compressed(os.path.join(HERE, "q8_0_dequant.npz"), q=q, d=d, out=out)
+
+
 if __name__ == "__main__":
     if not O.ref_available():
         O.build()
@@ -146,4 +165,5 @@ if __name__ == "__main__":
     gen_kvcache()
     gen_attn()
     gen_rope()
+    gen_q8()
     print("golden vectors written to", HERE)

@@ -1,0 +1,236 @@
+"""GPU parity of the Q8_0 cache against the CPU oracle (through the C ABI).
+
+Append / gather: bit-exact against oracle.c's Q8_0 quantizer (the
+reference's quantizer, gpu.cu:1077-1086, with the scale kept as binary16).
+Attention: within 2e-3 max-abs of the oracle's op_attn over the dequantized
+cache (quants.c:368-373), for the decode kernel (1..15 rows) and the MFMA
+prefill kernel (16+ rows), with slot tables, windows and rings.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def T():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import tlkv
+    tlkv.check(tlkv.lib().tl_init(0))
+    return torch
+
+
+_KEEP = []
+
+
+def dev(T, a):
+    """Device copy kept alive until the next sync (kernels run asynchronously)."""
+    t = T.from_numpy(np.ascontiguousarray(a)).cuda()
+    _KEEP.append(t)
+    return t
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def sync(T):
+    T.cuda.synchronize()
+    _KEEP.clear()
+
+
+def rows(rng, n, width, scale_spread=False):
+    x = rng.standard_normal((n, width)).astype(np.float32)
+    if scale_spread and n:
+        # blocks of very different magnitudes, zero blocks, exact ties
+        x *= rng.choice([1e-3, 0.1, 1.0, 30.0], size=(n, width // 32, 1)).repeat(32, 2).reshape(n, width)
+        x[0, :32] = 0.0
+        x[0, 32:64] = np.arange(32, dtype=np.float32) - 15.5
+        x[0, 64] = 127.0
+    return x
+
+
+def _q8(L):
+    return host(L.k), host(L.ks).view(np.uint16), host(L.v), host(L.vs).view(np.uint16)
+
+
+@pytest.mark.parametrize("n_kv,hd,cap,n,pos,perm,ring", [
+    (8, 128, 64, 17, 5, True, 0),
+    (8, 64, 40, 33, 0, False, 0),
+    (4, 256, 32, 9, 3, True, 0),
+    (4, 128, 600, 512, 7, True, 0),
+    (2, 128, 50, 40, 30, False, 50),     # wraps the ring once (no slot written twice)
+])
+def test_append_q8_bitexact(T, n_kv, hd, cap, n, pos, perm, ring):
+    import tlkv
+    rng = np.random.default_rng(n * 31 + hd)
+    k = rows(rng, n, n_kv * hd, scale_spread=True)
+    v = rows(rng, n, n_kv * hd, scale_spread=True)
+    slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    L = tlkv.LayerQ8(cap, n_kv, hd, ring=ring)
+    ds = None if ring else dev(T, slots)
+    tlkv.check(tlkv.lib().tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, k)), tlkv.ptr(dev(T, v)),
+                                          n_kv * hd, tlkv.ptr(ds), pos, n, None))
+    sync(T)
+    C = O.CacheQ8(cap, n_kv, hd, ring)
+    if ring:
+        for i in range(n):   # rows in order: later rows overwrite earlier ones
+            assert C.append(k[i:i + 1], v[i:i + 1], None, pos + i, 1) == 0
+    else:
+        assert C.append(k, v, slots, pos, n) == 0
+    gk, gks, gv, gvs = _q8(L)
+    assert np.array_equal(gk, C.k)
+    assert np.array_equal(gks, C.ks)
+    assert np.array_equal(gv, C.v)
+    assert np.array_equal(gvs, C.vs)
+
+
+def test_append_q8_out_of_range_slot_skipped(T):
+    import tlkv
+    rng = np.random.default_rng(5)
+    n_kv, hd, cap = 2, 64, 16
+    k = rows(rng, 4, n_kv * hd)
+    slots = np.array([3, 99, 7, 15], dtype=np.uint32)
+    L = tlkv.LayerQ8(cap, n_kv, hd)
+    tlkv.check(tlkv.lib().tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, k)), tlkv.ptr(dev(T, k)),
+                                          n_kv * hd, tlkv.ptr(dev(T, slots)), 0, 4, None))
+    sync(T)
+    gk = host(L.k)
+    q, d = O.q8_quantize(k.reshape(4, n_kv, hd))
+    for i, s in enumerate(slots):
+        if s < cap:
+            assert np.array_equal(gk[:, s], q[i])
+    untouched = [s for s in range(cap) if s not in (3, 7, 15)]
+    assert not gk[:, untouched].any()
+
+
+def test_gather_q8_roundtrip(T):
+    import tlkv
+    rng = np.random.default_rng(11)
+    n_kv, hd, cap = 4, 128, 100
+    k = rows(rng, cap, n_kv * hd, scale_spread=True)
+    v = rows(rng, cap, n_kv * hd, scale_spread=True)
+    L = tlkv.LayerQ8(cap, n_kv, hd)
+    tlkv.check(tlkv.lib().tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, k)), tlkv.ptr(dev(T, v)),
+                                          n_kv * hd, None, 0, cap, None))
+    sel = np.concatenate([rng.permutation(cap)[:37], [cap + 5]]).astype(np.uint32)
+    n = sel.size
+    ko = T.zeros((n, n_kv, hd), dtype=T.int8, device="cuda")
+    vo = T.zeros_like(ko)
+    kso = T.zeros((n, n_kv, hd // 32), dtype=T.int16, device="cuda")
+    vso = T.zeros_like(kso)
+    tlkv.check(tlkv.lib().tl_kv_gather_q8(L.desc, tlkv.ptr(dev(T, sel)), n, tlkv.ptr(ko),
+                                          tlkv.ptr(kso), tlkv.ptr(vo), tlkv.ptr(vso), None))
+    sync(T)
+    qk, dk = O.q8_quantize(k.reshape(cap, n_kv, hd))
+    qv, dv = O.q8_quantize(v.reshape(cap, n_kv, hd))
+    assert np.array_equal(host(ko)[:-1], qk[sel[:-1]])
+    assert np.array_equal(host(kso).view(np.uint16)[:-1], dk[sel[:-1]])
+    assert np.array_equal(host(vo)[:-1], qv[sel[:-1]])
+    assert np.array_equal(host(vso).view(np.uint16)[:-1], dv[sel[:-1]])
+    assert not host(ko)[-1].any() and not host(kso)[-1].any()   # slot outside the cache
+
+
+def _run_attn_q8(T, n_head, n_kv, hd, cap, pos, n, window, slots, seed, ring=0,
+                 append=True):
+    """Fill positions [0,pos) then run OP_ATTN over the Q8_0 cache on rows
+    [pos,pos+n) on the device and in the oracle.  Returns (device, oracle)."""
+    import tlkv
+    rng = np.random.default_rng(seed)
+    kd = n_kv * hd
+    total = pos + n
+    hk, hv = rows(rng, total, kd), rows(rng, total, kd)
+    q = rows(rng, n, n_head * hd)
+    L = tlkv.LayerQ8(cap, n_kv, hd, ring=ring)
+    C = O.CacheQ8(cap, n_kv, hd, ring)
+    ds = None if slots is None else dev(T, slots)
+    fill = total if not append else pos
+    lo = max(0, fill - ring) if ring else 0
+    if fill > lo:
+        tlkv.check(tlkv.lib().tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, hk[lo:fill])),
+                                              tlkv.ptr(dev(T, hv[lo:fill])), kd, tlkv.ptr(ds),
+                                              lo, fill - lo, None))
+        assert C.append(hk[lo:fill], hv[lo:fill], slots, lo, fill - lo) == 0
+    out = T.zeros((n, n_head * hd), dtype=T.float32, device="cuda")
+    dk, dv = (dev(T, hk[pos:]), dev(T, hv[pos:])) if append else (None, None)
+    a = tlkv.attn_args(dev(T, q), dk, dv, out, ds, pos, n, n_head, hd, n_kv, window,
+                       O.scale_of(hd))
+    fn = tlkv.lib().tl_attn_q8 if append else tlkv.lib().tl_attn_noappend_q8
+    tlkv.check(fn(L.desc, a, None))
+    sync(T)
+    ref = C.attn(q, hk[pos:] if append else None, hv[pos:] if append else None, slots, pos, n,
+                 n_head, window=window)
+    return host(out), ref, L, C
+
+
+Q8_CASES = [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted slots, ring
+    (32, 8, 64, 1024, 700, 1, 0, True, 0),       # config 1 shape
+    (28, 4, 128, 2048, 1500, 1, 0, True, 0),     # gqa 7
+    (32, 8, 128, 4096, 4000, 1, 0, False, 0),    # config 4 shape
+    (8, 4, 256, 2048, 1800, 1, 1024, True, 0),   # windowed, head_dim 256
+    (8, 4, 256, 1535, 3000, 1, 1024, False, 1535),   # ring
+    (32, 8, 128, 512, 0, 1, 0, False, 0),        # first token
+    (32, 8, 128, 512, 3, 1, 0, True, 0),         # tiny history
+    (16, 2, 128, 600, 200, 5, 0, True, 0),       # multi-row decode
+    (16, 2, 128, 600, 200, 15, 64, True, 0),     # multi-row + window
+    (8, 8, 64, 300, 100, 3, 0, False, 0),        # MHA
+    (24, 8, 128, 700, 500, 1, 0, True, 0),       # gqa 3
+    (40, 5, 128, 700, 500, 2, 0, True, 0),       # gqa 8
+    (16, 2, 128, 1200, 300, 200, 0, True, 0),    # prefill (MFMA, dequant on load)
+    (8, 4, 256, 1500, 700, 64, 256, False, 0),   # prefill, windowed, head_dim 256
+    (8, 1, 64, 600, 0, 333, 0, True, 0),         # prefill from empty
+]
+
+
+@pytest.mark.parametrize("case", Q8_CASES)
+def test_attn_q8_vs_oracle(T, case):
+    n_head, n_kv, hd, cap, pos, n, window, perm, ring = case
+    rng = np.random.default_rng(hash(case) & 0xffff)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    out, ref, L, C = _run_attn_q8(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                  seed=pos + n, ring=ring)
+    err = np.abs(out - ref).max()
+    assert err < TOL, f"vs Q8_0 oracle {err}"
+    # the batch rows were quantized into the cache bit-exactly
+    gk, gks, gv, gvs = _q8(L)
+    assert np.array_equal(gk, C.k) and np.array_equal(gks, C.ks)
+    assert np.array_equal(gv, C.v) and np.array_equal(gvs, C.vs)
+
+
+@pytest.mark.parametrize("n", [1, 4, 40])
+def test_attn_noappend_q8(T, n):
+    rng = np.random.default_rng(n)
+    cap = 900
+    slots = rng.permutation(cap).astype(np.uint32)
+    out, ref, _, _ = _run_attn_q8(T, 16, 4, 128, cap, 800, n, 0, slots, seed=n, append=False)
+    assert np.abs(out - ref).max() < TOL
+
+
+def test_attn_q8_full_size_config4(T):
+    """Config 4's shape at its full key count (one layer, last decode step)."""
+    out, ref, _, _ = _run_attn_q8(T, 32, 8, 128, 33800, 33791, 1, 0, None, seed=4)
+    assert np.abs(out - ref).max() < TOL
+
+
+def test_attn_q8_split_invariance(T):
+    """Different split counts (decode workgroups) give results within rounding."""
+    import os
+    rng = np.random.default_rng(9)
+    cap = 6000
+    slots = rng.permutation(cap).astype(np.uint32)
+    outs = []
+    for wgs in ("8", "64", ""):
+        os.environ["TL_DECODE_WGS"] = wgs
+        try:
+            out, ref, _, _ = _run_attn_q8(T, 32, 8, 128, cap, 5900, 1, 0, slots, seed=3)
+        finally:
+            os.environ.pop("TL_DECODE_WGS", None)
+        assert np.abs(out - ref).max() < TOL, wgs
+        outs.append(out)
+    assert np.abs(outs[0] - outs[2]).max() < 1e-3

@@ -142,3 +142,29 @@ TL_DEV uint4 cvt8_rope(const float *hrow, u32 e0, u32 pos, u32 rdim, float base,
     return make_uint4(pack_f16x2(t[0], t[1]), pack_f16x2(t[2], t[3]), pack_f16x2(t[4], t[5]),
                       pack_f16x2(t[6], t[7]));
 }
+
+/* ---- Q8_0 cache helpers ---------------------------------------------------- */
+
+typedef _Float16 tl_half2 __attribute__((ext_vector_type(2)));
+
+/* 4 int8 (element 0 in the low byte) -> f16 pairs (elements 0,1) and (2,3),
+ * exact: byte ^ 0x80 = q + 128 placed under the binary16 exponent of 1024
+ * (high byte 0x64) is the f16 value 1152 + q; one packed subtract leaves q. */
+TL_DEV void i8x4_to_f16(u32 w, tl_half2 &lo, tl_half2 &hi) {
+    const u32 x = w ^ 0x80808080u;
+    const tl_half2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(tl_half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - bias;
+    hi = __builtin_bit_cast(tl_half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - bias;
+}
+
+/* 8 int8 of one 32-element block and its binary16 scale d -> 8 binary16
+ * values RNE(q * d) (the product is formed exactly, then rounded once) */
+TL_DEV uint4 q8_dequant8(uint2 w, u32 d_bits) {
+    const tl_half2 d2 = __builtin_bit_cast(tl_half2, d_bits * 0x10001u);
+    tl_half2 a, b, c, e;
+    i8x4_to_f16(w.x, a, b);
+    i8x4_to_f16(w.y, c, e);
+    a *= d2; b *= d2; c *= d2; e *= d2;
+    return make_uint4(__builtin_bit_cast(u32, a), __builtin_bit_cast(u32, b),
+                      __builtin_bit_cast(u32, c), __builtin_bit_cast(u32, e));
+}

@@ -180,6 +180,27 @@ TL_DEV void lds_dma16(u32 m0, const void *base, u32 voff) {
                      :: "v"(voff), "s"(sb), "{m0}"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
 }
 
+/* One 4-byte-per-lane load straight into LDS (global_load_lds_dword):
+ * lane i's word lands at m0 + 4*i; otherwise as lds_dma16. */
+TL_DEV void lds_dma4(u32 m0, const void *base, u32 voff) {
+    const u64 g = (u64)base;
+    const u32 lo = __builtin_amdgcn_readfirstlane((u32)g);
+    const u32 hi = __builtin_amdgcn_readfirstlane((u32)(g >> 32));
+    const void *sb = (const void *)(((u64)hi << 32) | lo);
+    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1 nt"
+                     :: "v"(voff), "s"(sb), "{m0}"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
+}
+
+/* Q8_0 tiles: 6 loads each (K and V values 2 + 2, K and V scales 1 + 1) */
+TL_DEV void wait_tiles_q8(u32 n) {
+    switch (n) {
+    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: __asm__ volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 2: __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    default: __asm__ volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    }
+}
+
 /* wait until at most n tiles (8 loads each) are still in flight */
 TL_DEV void wait_tiles(u32 n) {
     switch (n) {
@@ -282,6 +303,96 @@ TL_DEV void ring_tile(const uint4 *tk, const uint4 *tv, const u32 (&qr)[G][8], u
         for (int h = 0; h < G; h++) {
             acc[h][2 * w] = __builtin_amdgcn_fdot2(lo, as_h2(pp[h]), acc[h][2 * w], false);
             acc[h][2 * w + 1] = __builtin_amdgcn_fdot2(hi, as_h2(pp[h]), acc[h][2 * w + 1], false);
+        }
+    }
+}
+
+/* ring_tile over a Q8_0 tile.  The tile's int8 rows are stored as loaded:
+ * row t holds D bytes = LPK 16-byte units, and lane (g, sub) reads unit sub
+ * of keys t0 = g and t1 = KPP + g (its 16 dims, as in ring_tile: one wave
+ * read covers 1 KB of consecutive LDS).  sk / sv hold the tile's binary16
+ * scales [TK][D/32]; the lane's 16 dims sit in block sub/2.
+ * Scores: the exact int8 values (f16) dot q, times the key's scale (f32).
+ * PV: V is dequantized to f16 (q * d rounded once) pairwise across the two
+ * keys, then v_dot2 with the packed probabilities as in ring_tile. */
+template <int D, int G>
+TL_DEV void ring_tile_q8(const uint4 *tk, const uint4 *tv, const u16 *sk, const u16 *sv,
+                         const u32 (&qr)[G][8], u32 tbase, u32 kend, int lane, float (&m)[G],
+                         float (&l)[G], float (&acc)[G][16]) {
+    using C = RCfg<D>;
+    constexpr int LPK = C::LPK, KPP = C::KPP, NB = D / 32;
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    const int g = lane / LPK, sub = lane % LPK;
+    const int t0 = g, t1 = KPP + g;
+    const uint4 ka = tk[t0 * LPK + sub], kb = tk[t1 * LPK + sub];
+    const float dk0 = (float)__builtin_bit_cast(_Float16, sk[t0 * NB + sub / 2]);
+    const float dk1 = (float)__builtin_bit_cast(_Float16, sk[t1 * NB + sub / 2]);
+    const u32 kaw[4] = {ka.x, ka.y, ka.z, ka.w}, kbw[4] = {kb.x, kb.y, kb.z, kb.w};
+    half2_t fa[8], fb[8];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        i8x4_to_f16(kaw[w], fa[2 * w], fa[2 * w + 1]);
+        i8x4_to_f16(kbw[w], fb[2 * w], fb[2 * w + 1]);
+    }
+    float s0[G], s1[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            a = __builtin_amdgcn_fdot2(fa[w], as_h2(qr[h][w]), a, false);
+            b = __builtin_amdgcn_fdot2(fb[w], as_h2(qr[h][w]), b, false);
+        }
+        s0[h] = a * dk0;
+        s1[h] = b * dk1;
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        s0[h] = group_sum<LPK>(s0[h]);
+        s1[h] = group_sum<LPK>(s1[h]);
+        __asm__ volatile("" : "+v"(s0[h]), "+v"(s1[h]));
+    }
+    const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        s0[h] = v0 ? s0[h] : NEG_INF;
+        s1[h] = v1 ? s1[h] : NEG_INF;
+    }
+    const uint4 va = tv[t0 * LPK + sub], vb = tv[t1 * LPK + sub];
+    const u32 dvb = (u32)sv[t0 * NB + sub / 2] | ((u32)sv[t1 * NB + sub / 2] << 16);
+    u32 pp[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float mx = fmaxf(s0[h], s1[h]);
+        if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
+            const float mn = group_max<64>(mx);
+            const float alpha = fast_exp2(m[h] - mn);
+            l[h] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
+            m[h] = mn;
+        }
+        const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
+        const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
+        l[h] += p0 + p1;
+        pp[h] = pack_f16x2_fast(p0, p1);
+    }
+    const half2_t dv2 = as_h2(dvb);                 /* (d of key t0, d of key t1) */
+    const u32 vaw[4] = {va.x, va.y, va.z, va.w}, vbw[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        /* bytes (a0 b0 a1 b1) and (a2 b2 a3 b3): key pairs of dims 4w .. 4w+3 */
+        const u32 x01 = __builtin_amdgcn_perm(vbw[w], vaw[w], 0x05010400u);
+        const u32 x23 = __builtin_amdgcn_perm(vbw[w], vaw[w], 0x07030602u);
+        half2_t e[4];
+        i8x4_to_f16(x01, e[0], e[1]);
+        i8x4_to_f16(x23, e[2], e[3]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const half2_t vv = e[k] * dv2;
+#pragma unroll
+            for (int h = 0; h < G; h++)
+                acc[h][4 * w + k] = __builtin_amdgcn_fdot2(vv, as_h2(pp[h]), acc[h][4 * w + k], false);
         }
     }
 }
@@ -390,22 +501,27 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
 #define TL_XCD_ROT 0
 #endif
 #define TL_RING_STAGES 2
-template <int D, int G, bool ROPE>
+template <int D, int G, bool ROPE, bool Q8>
 __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
     using C = RCfg<D>;
     constexpr int LPK = C::LPK, CPR = C::CPR, TK = C::TK, UNITS = C::UNITS, LD = C::LD;
-    constexpr int W = TL_RING_WAVES, S = TL_RING_STAGES, NT = 64 * W;
+    /* a Q8_0 tile is half the bytes of an f16 one: twice the stages in the
+     * same ring memory, plus the scales (64 words per stage) */
+    constexpr int W = TL_RING_WAVES, S = Q8 ? 2 * TL_RING_STAGES : TL_RING_STAGES, NT = 64 * W;
+    constexpr int STAGE_U = Q8 ? UNITS : 2 * UNITS;   /* 16-byte units per stage (K + V) */
+    constexpr int RING_U = 2 * TL_RING_STAGES * UNITS;
     constexpr int VPR = D / 8;
     constexpr float NEG_INF = -__builtin_huge_valf();
     static_assert(LD == 4, "wait_tiles assumes 8 loads per tile");
+    static_assert(S * STAGE_U <= RING_U, "ring stages");
 
-    __shared__ uint4 s_ring[W][S][2][UNITS];     /* per wave: S stages of (K, V) */
+    __shared__ uint4 s_ring[W][RING_U];          /* per wave: S stages of (K, V) */
+    __shared__ u32 s_scl[Q8 ? W : 1][Q8 ? S * 64 : 1];
     __shared__ u32 s_slot[TL_DEC_MAX_CHUNK];
     __shared__ uint4 s_q[G * D / 8];
     __shared__ float s_m[W][G];
-    __shared__ float s_l[W][G];
-    __shared__ uint4 s_newk[TL_DEC_MAX_NEW][D / 8];
-    __shared__ uint4 s_newv[TL_DEC_MAX_NEW][D / 8];
+    __shared__ uint4 s_newk[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
+    __shared__ uint4 s_newv[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -435,7 +551,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
     const u32 kbeg = start + split * p.chunk;
     const u32 kend = min(kbeg + p.chunk, n_keys);
-    const bool fused = sq.kin != nullptr;
+    const bool fused = !Q8 && sq.kin != nullptr;
     const bool writer = fused && split == 0 && r == 0;
     const bool need_new = fused && (writer || kend > sq.pos);
     const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
@@ -521,7 +637,13 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     const u16 *Kbase = sq.k + (u64)kvh * sq.cap * D;
     const u16 *Vbase = sq.v + (u64)kvh * sq.cap * D;
-    const u32 ring_lds = (u32)(uintptr_t)&s_ring[wave][0][0][0];
+    const u32 ring_lds = (u32)(uintptr_t)&s_ring[wave][0];
+    /* Q8_0: int8 rows and their scale planes (f16 [n_kv][cap][D/32]) */
+    const uint8_t *K8 = (const uint8_t *)sq.k + (u64)kvh * sq.cap * D;
+    const uint8_t *V8 = (const uint8_t *)sq.v + (u64)kvh * sq.cap * D;
+    const u16 *KS = Q8 ? sq.ks + (u64)kvh * sq.cap * (D / 32) : nullptr;
+    const u16 *VS = Q8 ? sq.vs + (u64)kvh * sq.cap * (D / 32) : nullptr;
+    const u32 scl_lds = (u32)(uintptr_t)&s_scl[Q8 ? wave : 0][0];
 
     /* tiles of the chunk: the first n_dma (entirely cache rows written
      * before this launch) stream through the ring; the rest hold new rows */
@@ -540,7 +662,29 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
      * scores are masked to -inf, so they add exactly 0). */
     auto issue = [&](u32 j) {
         const u32 tb = kbeg + (wave + W * j) * TK;
-        const u32 lk = ring_lds + (j % S) * (2 * UNITS * 16);
+        const u32 lk = ring_lds + (j % S) * (STAGE_U * 16);
+        if constexpr (Q8) {
+            /* values: unit u = jj*64 + lane is 16-byte unit u % LPK of tile
+             * row u / LPK, stored as loaded; K then V (UNITS/2 units each) */
+#pragma unroll
+            for (int jj = 0; jj < LD / 2; jj++) {
+                const int u = jj * 64 + lane;
+                const u32 ph = phys(min(tb + (u32)(u / LPK), klast));
+                const u32 off = ph * D + (u % LPK) * 16;
+                lds_dma16(lk + jj * 1024, K8, off);
+                lds_dma16(lk + UNITS * 8 + jj * 1024, V8, off);
+            }
+            /* scales: 32 words per plane (TK rows x D/32 f16), lanes 0..31 */
+            const int srow = lane / (D / 64), sw = lane % (D / 64);
+            const u32 sph = phys(min(tb + (u32)srow, klast));
+            const u32 soff = (sph * (D / 32) + 2 * sw) * 2;
+            const u32 ls = scl_lds + (j % S) * 256;
+            if (lane < 32) {
+                lds_dma4(ls, KS, soff);
+                lds_dma4(ls + 128, VS, soff);
+            }
+            return;
+        }
 #pragma unroll
         for (int jj = 0; jj < LD; jj++) {
             const int u = jj * 64 + lane;
@@ -577,21 +721,31 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     for (u32 j = 0; j < nj; j++) {
         const u32 after = nj - 1 - j;
-        wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
+        if constexpr (Q8)
+            wait_tiles_q8(after < (u32)(S - 1) ? after : (u32)(S - 1));
+        else
+            wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
 #ifdef TL_DEC_TRACE
         if (j == 0 && lane == 0 && blockIdx.x < 8192)
             tl_dec_trace[blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();
 #endif
 #ifndef TL_DEC_NOCOMPUTE
-        ring_tile<D, G>(s_ring[wave][j % S][0], s_ring[wave][j % S][1], qr,
-                        kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
+        const uint4 *st = &s_ring[wave][(j % S) * STAGE_U];
+        if constexpr (Q8) {
+            const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
+            ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
+                               kend, lane, m, l, acc);
+        } else {
+            ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
+        }
 #endif
         if (j + S < nj) issue(j + S);
     }
     /* tiles with new rows: cache rows and staged new rows through registers */
+    if constexpr (!Q8)
     for (u32 t = n_dma + ((u32)wave + W - n_dma % W) % W; t < ntile; t += W) {
-        uint4 *tk = s_ring[wave][0][0];
-        uint4 *tv = s_ring[wave][0][1];
+        uint4 *tk = &s_ring[wave][0];
+        uint4 *tv = &s_ring[wave][UNITS];
         const u32 tb = kbeg + t * TK;
 #pragma unroll
         for (int jj = 0; jj < LD; jj++) {
@@ -615,7 +769,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         ring_tile<D, G>(tk, tv, qr, tb, kend, lane, m, l, acc);
         __builtin_amdgcn_wave_barrier();
     }
-    if (writer) {
+    if (!Q8 && writer) {
         for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
             const u32 row = i / VPR, c8 = i % VPR;
             const u32 key = sq.pos + row;
@@ -643,11 +797,11 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
     constexpr int TPC0 = NT / COLB > GPW ? GPW : NT / COLB;
     constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
-    constexpr int WREG = S * 2 * UNITS;               /* float4 per wave region */
+    constexpr int WREG = RING_U;                      /* float4 per wave region */
     static_assert(HB * 4 * 64 <= WREG, "wave state exceeds its ring region");
     static_assert(GPW % TPC == 0, "lane groups per thread");
     __shared__ float s_lg[G][NGRP];
-    float4 *s_w4 = (float4 *)&s_ring[0][0][0][0];
+    float4 *s_w4 = (float4 *)&s_ring[0][0];
     const int sub = lane % LPK, gi = lane / LPK;
 #pragma unroll
     for (int h = 0; h < G; h++) {
@@ -754,7 +908,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     TL_TRACE(9);
     /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */
-    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0][0][0]);
+    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0]);
 #ifdef TL_DEC_TRACE
     __syncthreads();
     TL_TRACE(4);
@@ -771,13 +925,14 @@ struct DecKernel {
 };
 
 template <int D>
-static DecKernel pick_kernel(int G, bool rope) {
+static DecKernel pick_kernel(int G, bool rope, bool q8) {
     constexpr int NT = 64 * TL_RING_WAVES;
     switch (G) {
-#define TL_CASE(g)                                                                       \
-    case g:                                                                              \
-        if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true>, 4096, NT};  \
-        return {(const void *)attn_decode_ring_kernel<D, g, false>, 4096, NT};
+#define TL_CASE(g)                                                                          \
+    case g:                                                                                 \
+        if (q8) return {(const void *)attn_decode_ring_kernel<D, g, false, true>, 4096, NT}; \
+        if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true, false>, 4096, NT}; \
+        return {(const void *)attn_decode_ring_kernel<D, g, false, false>, 4096, NT};
         TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
         TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
 #undef TL_CASE
@@ -827,12 +982,17 @@ static int resident_per_cu(const void *fn, int threads) {
  * are merged by the group's last workgroup when they fit its LDS, else by
  * attn_merge_kernel. */
 int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
-                     u32 max_vis, hipStream_t st) {
+                     u32 max_vis, hipStream_t st, bool q8) {
+    if (q8) {
+        if (p.rope.rdim) return tl_fail(TL_EINVAL, "decode: no fused RoPE over a Q8_0 cache");
+        for (u32 i = 0; i < TL_MAX_BATCH_SEQ; i++)
+            if (p.seq[i].kin) return tl_fail(TL_EINVAL, "decode: no fused append into a Q8_0 cache");
+    }
     DecKernel K;
     switch (head_dim) {
-    case 64: K = pick_kernel<64>((int)G, p.rope.rdim != 0); break;
-    case 128: K = pick_kernel<128>((int)G, p.rope.rdim != 0); break;
-    case 256: K = pick_kernel<256>((int)G, p.rope.rdim != 0); break;
+    case 64: K = pick_kernel<64>((int)G, p.rope.rdim != 0, q8); break;
+    case 128: K = pick_kernel<128>((int)G, p.rope.rdim != 0, q8); break;
+    case 256: K = pick_kernel<256>((int)G, p.rope.rdim != 0, q8); break;
     default: return tl_fail(TL_EINVAL, "head_dim %u", head_dim);
     }
     if (!K.fn) return tl_fail(TL_EINVAL, "gqa ratio %u unsupported (1..8)", G);

@@ -37,7 +37,8 @@ struct CopyParams {
 
 /* One sequence of a decode launch (rows_per_seq rows at positions pos..). */
 struct DecSeq {
-    const uint16_t *k, *v;
+    const uint16_t *k, *v;    /* f16 rows, or int8 rows of a Q8_0 cache */
+    const uint16_t *ks, *vs;  /* Q8_0 scales (f16 [n_kv][cap][D/32]), else NULL */
     const uint32_t *slots;
     const float *q;
     float *dst;
@@ -59,7 +60,8 @@ struct DecParams {
 
 /* Chunked-prefill launch (one OP_ATTN batch of one session). */
 struct PrefParams {
-    const uint16_t *k, *v;
+    const uint16_t *k, *v;    /* f16 rows, or int8 rows of a Q8_0 cache */
+    const uint16_t *ks, *vs;  /* Q8_0 scales, else NULL */
     const uint32_t *slots;
     uint32_t cap, ring;
     const float *q;
@@ -79,6 +81,18 @@ struct TlWorkspace {
     size_t acc_cap, ml_cap, cnt_cap;
 };
 
+/* A layer's storage as the attention launches read it: an f16 cache
+ * (tl_kv_layer) or a Q8_0 cache (tl_kv_layer_q8, q8 = true). */
+struct LayerView {
+    const void *k, *v;
+    const uint16_t *ks, *vs;
+    uint32_t cap, n_kv_head, head_dim, ring;
+    bool q8;
+};
+LayerView tl_view(const tl_kv_layer *L);
+int tl_check_attn_args(const LayerView &L, const tl_attn_args *a);
+int tl_rope_cfg(uint32_t head_dim, const tl_rope_params *r, RopeCfg &c);
+
 int tl_fail(int code, const char *fmt, ...);
 
 #define HIP_TRY(expr)                                                         \
@@ -92,12 +106,13 @@ int tl_fail(int code, const char *fmt, ...);
 #define TL_DEC_MAX_CHUNK 2048
 int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters, TlWorkspace **out);
 int tl_launch_append(const AppendParams &p, uint32_t n_seg, hipStream_t stream);
+/* q8: the seq[] rows are a Q8_0 cache (no fused append: kin must be NULL) */
 int tl_launch_decode(DecParams &p, uint32_t n_rows_total, uint32_t head_dim, uint32_t G,
-                     uint32_t max_vis, hipStream_t st);
+                     uint32_t max_vis, hipStream_t st, bool q8 = false);
 /* combine n_split partial rows (ws_acc / ws_ml) into seq[..].dst */
 int tl_launch_merge(const DecParams &p, uint32_t n_rows_total, uint32_t head_dim, hipStream_t st);
 
 /* MFMA chunked-prefill attention (tl_prefill.hip). */
-bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a);
-int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, const RopeCfg &rope,
+bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a);
+int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &rope,
                       hipStream_t st);

@@ -242,17 +242,21 @@ extern "C" int tl_kv_append(const tl_kv_layer *L, const float *k, const float *v
     return tl_launch_append(p, 1, (hipStream_t)stream);
 }
 
-static int rope_cfg(const tl_kv_layer *L, const tl_rope_params *r, RopeCfg &c) {
+int tl_rope_cfg(uint32_t head_dim, const tl_rope_params *r, RopeCfg &c) {
     c.rdim = 0;
     c.theta = 0.f;
     c.neox = 0;
     if (!r) return TL_OK;
-    if (r->rope_dim > L->head_dim || (r->rope_dim & 1) || !(r->theta > 0.f))
+    if (r->rope_dim > head_dim || (r->rope_dim & 1) || !(r->theta > 0.f))
         return tl_fail(TL_EINVAL, "rope: dim %u theta %g", r->rope_dim, (double)r->theta);
     c.rdim = r->rope_dim;
     c.theta = r->theta;
     c.neox = r->neox ? 1 : 0;
     return TL_OK;
+}
+
+static int rope_cfg(const tl_kv_layer *L, const tl_rope_params *r, RopeCfg &c) {
+    return tl_rope_cfg(L->head_dim, r, c);
 }
 
 extern "C" int tl_kv_append_rope(const tl_kv_layer *L, const float *k, const float *v,
@@ -437,26 +441,45 @@ extern "C" int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t he
 /* OP_ATTN entry points                                                      */
 /* ------------------------------------------------------------------------ */
 
+LayerView tl_view(const tl_kv_layer *L) {
+    LayerView v;
+    v.k = L->k;
+    v.v = L->v;
+    v.ks = v.vs = nullptr;
+    v.cap = L->cap;
+    v.n_kv_head = L->n_kv_head;
+    v.head_dim = L->head_dim;
+    v.ring = L->ring;
+    v.q8 = false;
+    return v;
+}
+
+/* OP_ATTN argument rules shared by the f16 and Q8_0 caches (the layer
+ * itself has been checked) */
+int tl_check_attn_args(const LayerView &L, const tl_attn_args *a) {
+    if (!a || !a->q || !a->dst) return tl_fail(TL_EINVAL, "attn: null q/dst");
+    if (a->n_head == 0 || a->n_head % L.n_kv_head)
+        return tl_fail(TL_EINVAL, "attn: n_head %u not a multiple of n_kv %u",
+                       a->n_head, L.n_kv_head);
+    if (a->n_head / L.n_kv_head > 8)
+        return tl_fail(TL_EINVAL, "attn: gqa ratio %u > 8", a->n_head / L.n_kv_head);
+    if (a->q_stride < a->n_head * L.head_dim || (a->q_stride & 3) ||
+        (((uintptr_t)a->q | (uintptr_t)a->dst) & 15))
+        return tl_fail(TL_EINVAL, "attn: q/dst rows must be 16-byte aligned");
+    if (L.ring) {
+        if (!a->window || L.ring < a->window + a->n - 1)
+            return tl_fail(TL_EINVAL, "attn: ring %u too small for window %u and %u rows",
+                           L.ring, a->window, a->n);
+    } else if (!a->slots && (u64)a->pos + a->n > L.cap) {
+        return tl_fail(TL_ERANGE, "attn: pos %u + n %u exceeds cap %u", a->pos, a->n, L.cap);
+    }
+    return TL_OK;
+}
+
 static int check_args(const tl_kv_layer *L, const tl_attn_args *a) {
     int rc = check_layer(L);
     if (rc) return rc;
-    if (!a || !a->q || !a->dst) return tl_fail(TL_EINVAL, "attn: null q/dst");
-    if (a->n_head == 0 || a->n_head % L->n_kv_head)
-        return tl_fail(TL_EINVAL, "attn: n_head %u not a multiple of n_kv %u",
-                       a->n_head, L->n_kv_head);
-    if (a->n_head / L->n_kv_head > 8)
-        return tl_fail(TL_EINVAL, "attn: gqa ratio %u > 8", a->n_head / L->n_kv_head);
-    if (a->q_stride < a->n_head * L->head_dim || (a->q_stride & 3) ||
-        (((uintptr_t)a->q | (uintptr_t)a->dst) & 15))
-        return tl_fail(TL_EINVAL, "attn: q/dst rows must be 16-byte aligned");
-    if (L->ring) {
-        if (!a->window || L->ring < a->window + a->n - 1)
-            return tl_fail(TL_EINVAL, "attn: ring %u too small for window %u and %u rows",
-                           L->ring, a->window, a->n);
-    } else if (!a->slots && (u64)a->pos + a->n > L->cap) {
-        return tl_fail(TL_ERANGE, "attn: pos %u + n %u exceeds cap %u", a->pos, a->n, L->cap);
-    }
-    return TL_OK;
+    return tl_check_attn_args(tl_view(L), a);
 }
 
 /* append (when `append`) + attention.  Decode-sized batches run as one
@@ -464,7 +487,8 @@ static int check_args(const tl_kv_layer *L, const tl_attn_args *a) {
  * ones append first and then run the MFMA kernel. */
 static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
                      const RopeCfg &rope, hipStream_t st) {
-    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(L, a)) {
+    const LayerView lv = tl_view(L);
+    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(lv, a)) {
         if (append) {
             AppendParams ap;
             memset(&ap, 0, sizeof(ap));
@@ -474,7 +498,7 @@ static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
             rc = tl_launch_append(ap, 1, st);
             if (rc) return rc;
         }
-        return tl_launch_prefill(L, a, rope, st);
+        return tl_launch_prefill(lv, a, rope, st);
     }
     DecParams p;
     memset(&p, 0, sizeof(p));

@@ -77,7 +77,7 @@ TL_DEV uint2 ld_tr16(const _Float16 *lds_ptr) {
     return make_uint2(lo, hi);
 }
 
-template <int D, int G, bool ROPE>
+template <int D, int G, bool ROPE, bool Q8>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * PCfg<D, G>::W))) void attn_prefill_kernel(const PrefParams p) {
     using C = PCfg<D, G>;
     constexpr int W = C::W, ROWS = C::ROWS, BN = C::BN;
@@ -153,9 +153,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
 
     const u16 *Kb = p.k + (u64)kvh * p.cap * D;
     const u16 *Vb = p.v + (u64)kvh * p.cap * D;
+    /* Q8_0 cache: int8 rows and one f16 scale per 32 elements */
+    const uint8_t *K8 = (const uint8_t *)p.k + (u64)kvh * p.cap * D;
+    const uint8_t *V8 = (const uint8_t *)p.v + (u64)kvh * p.cap * D;
+    const u16 *Ksc = Q8 ? p.ks + (u64)kvh * p.cap * (D / 32) : nullptr;
+    const u16 *Vsc = Q8 ? p.vs + (u64)kvh * p.cap * (D / 32) : nullptr;
 
     /* register staging of one tile: unit u = tid + j*T -> row u / CPR,
-     * chunk u % CPR; rows past ke load zeros */
+     * chunk u % CPR; rows past ke load zeros.  A Q8_0 cache's units are
+     * dequantized here (8 int8 and their block's scale -> 8 f16). */
     uint4 rk[UPT], rv[UPT];
     auto load_tile = [&](u32 tb) __attribute__((always_inline)) {
 #pragma unroll
@@ -168,8 +174,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
             if (u < UNITS && key < ke) {
                 u32 ph = p.ring ? key % p.ring : (p.slots ? p.slots[key] : key);
                 ph = ph < p.cap ? ph : 0;
-                rk[j] = *(const uint4 *)(Kb + (u64)ph * D + c * 8);
-                rv[j] = *(const uint4 *)(Vb + (u64)ph * D + c * 8);
+                if constexpr (Q8) {
+                    const u64 e = (u64)ph * D + c * 8, sc = (u64)ph * (D / 32) + c / 4;
+                    rk[j] = q8_dequant8(*(const uint2 *)(K8 + e), Ksc[sc]);
+                    rv[j] = q8_dequant8(*(const uint2 *)(V8 + e), Vsc[sc]);
+                } else {
+                    rk[j] = *(const uint4 *)(Kb + (u64)ph * D + c * 8);
+                    rv[j] = *(const uint4 *)(Vb + (u64)ph * D + c * 8);
+                }
             }
         }
     };
@@ -312,20 +324,21 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
 
 /* ------------------------------------------------------------------------ */
 
-bool tl_prefill_supported(const tl_kv_layer *L, const tl_attn_args *a) {
+bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a) {
     if (getenv("TL_NO_PREFILL")) return false;
-    const u32 G = a->n_head / L->n_kv_head;
-    return (L->head_dim == 64 || L->head_dim == 128 || L->head_dim == 256) && G >= 1 && G <= 8;
+    const u32 G = a->n_head / L.n_kv_head;
+    return (L.head_dim == 64 || L.head_dim == 128 || L.head_dim == 256) && G >= 1 && G <= 8;
 }
 
 template <int D, int G>
 static void launch_pf(const PrefParams &p, u32 blocks, hipStream_t st) {
-    if (p.rope.rdim)
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true>), dim3(blocks),
-                           dim3(64 * PCfg<D, G>::W), 0, st, p);
+    const dim3 nt(64 * PCfg<D, G>::W);
+    if (p.ks)   /* Q8_0 cache (no RoPE fusion on this path) */
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false, true>), dim3(blocks), nt, 0, st, p);
+    else if (p.rope.rdim)
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true, false>), dim3(blocks), nt, 0, st, p);
     else
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false>), dim3(blocks),
-                           dim3(64 * PCfg<D, G>::W), 0, st, p);
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false, false>), dim3(blocks), nt, 0, st, p);
 }
 
 template <int D>
@@ -351,23 +364,27 @@ static u32 rows_per_wg(u32 D, u32 G) {
     return 32 * qb;
 }
 
-int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, const RopeCfg &rope,
+int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &rope,
                       hipStream_t st) {
-    const u32 D = L->head_dim, G = a->n_head / L->n_kv_head;
+    const u32 D = L.head_dim, G = a->n_head / L.n_kv_head;
+    if (L.q8 && (rope.rdim || !L.ks || !L.vs))
+        return tl_fail(TL_EINVAL, "prefill: a Q8_0 cache takes scales and no fused RoPE");
     PrefParams p;
     memset(&p, 0, sizeof(p));
-    p.k = (const u16 *)L->k;
-    p.v = (const u16 *)L->v;
+    p.k = (const u16 *)L.k;
+    p.v = (const u16 *)L.v;
+    p.ks = L.ks;
+    p.vs = L.vs;
     p.slots = a->slots;
-    p.cap = L->cap;
-    p.ring = L->ring;
+    p.cap = L.cap;
+    p.ring = L.ring;
     p.q = a->q;
     p.dst = a->dst;
     p.q_stride = a->q_stride;
     p.pos = a->pos;
     p.n = a->n;
     p.n_head = a->n_head;
-    p.n_kv = L->n_kv_head;
+    p.n_kv = L.n_kv_head;
     p.window = a->window;
     p.scale_log2 = a->scale * 1.4426950408889634f;
     p.rope = rope;
@@ -381,7 +398,7 @@ int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, const RopeCfg
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
             cus = n;
     }
-    const u32 base = nqb * L->n_kv_head;
+    const u32 base = nqb * L.n_kv_head;
     const u32 span = a->pos + a->n;        /* most keys any workgroup sees */
     u32 ns = (u32)((cus + base - 1) / base);
     const u32 max_ns = (span + 511) / 512;  /* keep >= 512 keys per split */
@@ -411,7 +428,7 @@ int tl_launch_prefill(const tl_kv_layer *L, const tl_attn_args *a, const RopeCfg
     memset(&mp, 0, sizeof(mp));
     mp.seq[0].dst = a->dst;
     mp.rows_per_seq = a->n;
-    mp.n_kv = L->n_kv_head;
+    mp.n_kv = L.n_kv_head;
     mp.n_head = a->n_head;
     mp.q_stride = a->q_stride;
     mp.n_split = ns;

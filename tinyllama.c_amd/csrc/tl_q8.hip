@@ -1,0 +1,302 @@
+/*
+ * tl_q8.hip — the Q8_0 KV cache: storage, quantizing append, gather and the
+ * OP_ATTN entry points over it.
+ *
+ * The reference's cache is f32 (src/def.h:289-294) and its notes list a
+ * quantized KV cache as missing (REMEMBER.md:18).  This cache keeps each
+ * row of each kv-head as blocks of 32 values in the GGUF Q8_0 form the
+ * reference dequantizes (src/quants.c:368-373: value = q * d, q int8, d
+ * binary16), planar so rows stay 16-byte aligned for the DMA loads:
+ *   k, v    int8 [n_kv][cap][head_dim]
+ *   ks, vs  f16  [n_kv][cap][head_dim / 32]
+ * Quantization is the reference's Q8_0 quantizer
+ * (src/backend/gpu/gpu.cu:1077-1086): amax = max |x|, d = amax / 127,
+ * id = d > 0 ? 1/d : 0, q = rint(x * id); d is stored RNE as binary16.
+ *
+ *   kv_append_q8_kernel  8 lanes per 32-element block: one float4 of K and
+ *                        of V each, the block max by DPP within the 8 lanes,
+ *                        one 4-byte store of q per lane, lane 0 the scale.
+ *   kv_gather_q8_kernel  rows by slot (values and scales).
+ * Attention: decode-sized batches run the split-K ring kernel's Q8_0
+ * instance (tl_decode.hip), larger ones the MFMA prefill kernel, which
+ * dequantizes its tiles to f16 as it stages them (tl_prefill.hip).
+ */
+#include "tl_common.h"
+#include "tl_internal.h"
+#include "../../include/tlkv.h"
+
+#include <string.h>
+
+static int check_layer_q8(const tl_kv_layer_q8 *L) {
+    if (!L || !L->k || !L->v || !L->ks || !L->vs)
+        return tl_fail(TL_EINVAL, "q8 layer: null storage");
+    if (L->head_dim != 64 && L->head_dim != 128 && L->head_dim != 256)
+        return tl_fail(TL_EINVAL, "head_dim %u unsupported (64/128/256)", L->head_dim);
+    if (L->n_kv_head == 0 || L->cap == 0) return tl_fail(TL_EINVAL, "q8 layer: empty shape");
+    if (L->ring > L->cap) return tl_fail(TL_EINVAL, "ring %u > cap %u", L->ring, L->cap);
+    if ((u64)L->cap * L->head_dim > 0xFFFFFFFFull)
+        return tl_fail(TL_ERANGE, "q8 layer: %u rows of head_dim %u exceed 4 GiB per kv-head",
+                       L->cap, L->head_dim);
+    if (((uintptr_t)L->k | (uintptr_t)L->v) & 15)
+        return tl_fail(TL_EINVAL, "q8 cache values not 16-byte aligned");
+    if (((uintptr_t)L->ks | (uintptr_t)L->vs) & 3)
+        return tl_fail(TL_EINVAL, "q8 cache scales not 4-byte aligned");
+    return TL_OK;
+}
+
+static LayerView view_q8(const tl_kv_layer_q8 *L) {
+    LayerView v;
+    v.k = L->k;
+    v.v = L->v;
+    v.ks = (const u16 *)L->ks;
+    v.vs = (const u16 *)L->vs;
+    v.cap = L->cap;
+    v.n_kv_head = L->n_kv_head;
+    v.head_dim = L->head_dim;
+    v.ring = L->ring;
+    v.q8 = true;
+    return v;
+}
+
+extern "C" int tl_kv_layer_alloc_q8(tl_kv_layer_q8 *L, uint32_t cap, uint32_t n_kv_head,
+                                    uint32_t head_dim, uint32_t ring) {
+    if (!L) return tl_fail(TL_EINVAL, "null layer");
+    memset(L, 0, sizeof(*L));
+    if (head_dim % 32) return tl_fail(TL_EINVAL, "head_dim %u not a multiple of 32", head_dim);
+    const size_t vb = (size_t)cap * n_kv_head * head_dim;
+    const size_t sb = vb / 32 * sizeof(u16);
+    if (vb == 0) return tl_fail(TL_EINVAL, "empty layer");
+    void **p[4] = {&L->k, &L->v, &L->ks, &L->vs};
+    const size_t bytes[4] = {vb, vb, sb, sb};
+    for (int i = 0; i < 4; i++) {
+        if (hipMalloc(p[i], bytes[i]) != hipSuccess) {
+            *p[i] = NULL;
+            tl_kv_layer_free_q8(L);
+            return tl_fail(TL_ENOMEM, "q8 layer: %zu bytes", bytes[i]);
+        }
+        HIP_TRY(hipMemset(*p[i], 0, bytes[i]));
+    }
+    L->cap = cap;
+    L->n_kv_head = n_kv_head;
+    L->head_dim = head_dim;
+    L->ring = ring;
+    return check_layer_q8(L);
+}
+
+extern "C" int tl_kv_layer_free_q8(tl_kv_layer_q8 *L) {
+    if (!L) return TL_OK;
+    void **p[4] = {&L->k, &L->v, &L->ks, &L->vs};
+    for (int i = 0; i < 4; i++) {
+        if (*p[i]) HIP_TRY(hipFree(*p[i]));
+        *p[i] = NULL;
+    }
+    return TL_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* quantizing append                                                         */
+/* ------------------------------------------------------------------------ */
+
+struct Q8AppendParams {
+    int8_t *k8, *v8;
+    u16 *ks, *vs;
+    const float *k, *v;
+    const u32 *slots;
+    u32 cap, ring, n_kv, head_dim, kv_stride, pos, n;
+};
+
+/* 4 values of a block whose scale is 1/id -> 4 int8 in one word */
+TL_DEV u32 q8_pack4(float4 x, float id) {
+    const int a = (int)rintf(x.x * id), b = (int)rintf(x.y * id);
+    const int c = (int)rintf(x.z * id), d = (int)rintf(x.w * id);
+    return (u32)(a & 0xff) | ((u32)(b & 0xff) << 8) | ((u32)(c & 0xff) << 16) |
+           ((u32)(d & 0xff) << 24);
+}
+
+TL_DEV float amax4(float4 x) {
+    return fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+}
+
+/* One lane per 4 elements; the 8 lanes of a block are an aligned group of
+ * a wave (grid stride and row length are multiples of 8), so the block max
+ * is a DPP max within the group. */
+__global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams p) {
+    const u32 qpr = p.head_dim >> 2;
+    const u64 total = (u64)p.n * p.n_kv * qpr;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        const u32 e = (u32)(idx % qpr);
+        const u64 t = idx / qpr;
+        const u32 h = (u32)(t % p.n_kv);
+        const u32 i = (u32)(t / p.n_kv);
+        const u64 src = (u64)i * p.kv_stride + (u64)h * p.head_dim + e * 4;
+        const float4 kx = *(const float4 *)(p.k + src);
+        const float4 vx = *(const float4 *)(p.v + src);
+        const float kmax = group_max<8>(amax4(kx));
+        const float vmax = group_max<8>(amax4(vx));
+        const u32 key = p.pos + i;
+        const u32 slot = p.ring ? key % p.ring : (p.slots ? p.slots[key] : key);
+        if (slot >= p.cap) continue;
+        const float dk = kmax / 127.0f, dv = vmax / 127.0f;
+        const float ik = dk > 0.0f ? 1.0f / dk : 0.0f;
+        const float iv = dv > 0.0f ? 1.0f / dv : 0.0f;
+        const u64 row = (u64)h * p.cap + slot;
+        *(u32 *)(p.k8 + row * p.head_dim + e * 4) = q8_pack4(kx, ik);
+        *(u32 *)(p.v8 + row * p.head_dim + e * 4) = q8_pack4(vx, iv);
+        if ((e & 7) == 0) {
+            p.ks[row * (p.head_dim / 32) + e / 8] = (u16)f32_to_f16_bits(dk);
+            p.vs[row * (p.head_dim / 32) + e / 8] = (u16)f32_to_f16_bits(dv);
+        }
+    }
+}
+
+static int append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v, u32 kv_stride,
+                     const u32 *slots, u32 pos, u32 n, hipStream_t st) {
+    if (n == 0) return TL_OK;
+    if (!k || !v) return tl_fail(TL_EINVAL, "append: null rows");
+    if (kv_stride < L->n_kv_head * L->head_dim || (kv_stride & 3) ||
+        (((uintptr_t)k | (uintptr_t)v) & 15))
+        return tl_fail(TL_EINVAL, "append: rows must be 16-byte aligned, stride %u", kv_stride);
+    Q8AppendParams p;
+    p.k8 = (int8_t *)L->k;
+    p.v8 = (int8_t *)L->v;
+    p.ks = (u16 *)L->ks;
+    p.vs = (u16 *)L->vs;
+    p.k = k;
+    p.v = v;
+    p.slots = slots;
+    p.cap = L->cap;
+    p.ring = L->ring;
+    p.n_kv = L->n_kv_head;
+    p.head_dim = L->head_dim;
+    p.kv_stride = kv_stride;
+    p.pos = pos;
+    p.n = n;
+    const u64 total = (u64)n * L->n_kv_head * (L->head_dim / 4);
+    u64 blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(kv_append_q8_kernel, dim3((u32)blocks), dim3(256), 0, st, p);
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+extern "C" int tl_kv_append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v,
+                               uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                               uint32_t n, void *stream) {
+    int rc = check_layer_q8(L);
+    if (rc) return rc;
+    return append_q8(L, k, v, kv_stride, slots, pos, n, (hipStream_t)stream);
+}
+
+/* ------------------------------------------------------------------------ */
+/* gather                                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* one thread per 16 values (and, for the first of a block's two, its scale) */
+__global__ __launch_bounds__(256) void kv_gather_q8_kernel(
+    const int8_t *k8, const int8_t *v8, const u16 *ks, const u16 *vs, u32 cap, u32 n_kv,
+    u32 head_dim, const u32 *slots, u32 n, int8_t *ko, u16 *kso, int8_t *vo, u16 *vso) {
+    const u32 upr = head_dim >> 4;
+    const u64 total = (u64)n * n_kv * upr;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        const u32 c = (u32)(idx % upr);
+        const u64 t = idx / upr;
+        const u32 h = (u32)(t % n_kv);
+        const u32 i = (u32)(t / n_kv);
+        const u32 slot = slots[i];
+        uint4 kk = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+        u16 a = 0, b = 0;
+        const bool ok = slot < cap;
+        if (ok) {
+            const u64 src = ((u64)h * cap + slot) * head_dim + c * 16;
+            kk = *(const uint4 *)(k8 + src);
+            vv = *(const uint4 *)(v8 + src);
+        }
+        const u64 dst = ((u64)i * n_kv + h) * head_dim + c * 16;
+        *(uint4 *)(ko + dst) = kk;
+        *(uint4 *)(vo + dst) = vv;
+        if ((c & 1) == 0) {
+            if (ok) {
+                a = ks[((u64)h * cap + slot) * (head_dim / 32) + c / 2];
+                b = vs[((u64)h * cap + slot) * (head_dim / 32) + c / 2];
+            }
+            kso[dst / 32] = a;
+            vso[dst / 32] = b;
+        }
+    }
+}
+
+extern "C" int tl_kv_gather_q8(const tl_kv_layer_q8 *L, const uint32_t *slots, uint32_t n,
+                               int8_t *k_out, uint16_t *ks_out, int8_t *v_out,
+                               uint16_t *vs_out, void *stream) {
+    int rc = check_layer_q8(L);
+    if (rc) return rc;
+    if (n == 0) return TL_OK;
+    if (!slots || !k_out || !v_out || !ks_out || !vs_out)
+        return tl_fail(TL_EINVAL, "gather: null pointer");
+    if (((uintptr_t)k_out | (uintptr_t)v_out) & 15)
+        return tl_fail(TL_EINVAL, "gather: outputs not 16-byte aligned");
+    const u64 total = (u64)n * L->n_kv_head * (L->head_dim / 16);
+    u64 blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(kv_gather_q8_kernel, dim3((u32)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const int8_t *)L->k, (const int8_t *)L->v, (const u16 *)L->ks,
+                       (const u16 *)L->vs, L->cap, L->n_kv_head, L->head_dim, slots, n, k_out,
+                       ks_out, v_out, vs_out);
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* OP_ATTN over a Q8_0 cache                                                 */
+/* ------------------------------------------------------------------------ */
+
+static int attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, bool append,
+                   hipStream_t st) {
+    int rc = check_layer_q8(L);
+    if (rc) return rc;
+    const LayerView lv = view_q8(L);
+    rc = tl_check_attn_args(lv, a);
+    if (rc) return rc;
+    if (a->n == 0) return TL_OK;
+    if (append) {
+        rc = append_q8(L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n, st);
+        if (rc) return rc;
+    }
+    RopeCfg none;
+    tl_rope_cfg(L->head_dim, nullptr, none);
+    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(lv, a))
+        return tl_launch_prefill(lv, a, none, st);
+    DecParams p;
+    memset(&p, 0, sizeof(p));
+    p.seq[0].k = (const u16 *)L->k;
+    p.seq[0].v = (const u16 *)L->v;
+    p.seq[0].ks = (const u16 *)L->ks;
+    p.seq[0].vs = (const u16 *)L->vs;
+    p.seq[0].slots = a->slots;
+    p.seq[0].q = a->q;
+    p.seq[0].dst = a->dst;
+    p.seq[0].cap = L->cap;
+    p.seq[0].ring = L->ring;
+    p.seq[0].pos = a->pos;
+    p.rows_per_seq = a->n;
+    p.n_kv = L->n_kv_head;
+    p.n_head = a->n_head;
+    p.q_stride = a->q_stride;
+    p.window = a->window;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.rope = none;
+    const u32 max_keys = a->pos + a->n;
+    const u32 max_vis = (a->window && max_keys > a->window) ? a->window : max_keys;
+    return tl_launch_decode(p, a->n, L->head_dim, a->n_head / L->n_kv_head, max_vis, st, true);
+}
+
+extern "C" int tl_attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *stream) {
+    return attn_q8(L, a, true, (hipStream_t)stream);
+}
+
+extern "C" int tl_attn_noappend_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a,
+                                   void *stream) {
+    return attn_q8(L, a, false, (hipStream_t)stream);
+}

@@ -20,6 +20,11 @@ class KvLayer(ctypes.Structure):
                 ("head_dim", u32), ("ring", u32)]
 
 
+class KvLayerQ8(ctypes.Structure):
+    _fields_ = [("k", vp), ("v", vp), ("ks", vp), ("vs", vp), ("cap", u32),
+                ("n_kv_head", u32), ("head_dim", u32), ("ring", u32)]
+
+
 class AttnArgs(ctypes.Structure):
     _fields_ = [("q", vp), ("k", vp), ("v", vp), ("dst", vp), ("slots", vp),
                 ("pos", u32), ("n", u32), ("n_head", u32), ("q_stride", u32),
@@ -76,6 +81,12 @@ def lib():
         "tl_rope": [vp, u32, u32, u32, u32, u32, u32, ctypes.c_float,
                     ctypes.c_int, vp],
         "tl_probe_read": [vp, ctypes.c_uint64, vp, u32, u32, vp],
+        "tl_kv_layer_alloc_q8": [ctypes.POINTER(KvLayerQ8), u32, u32, u32, u32],
+        "tl_kv_layer_free_q8": [ctypes.POINTER(KvLayerQ8)],
+        "tl_kv_append_q8": [ctypes.POINTER(KvLayerQ8), vp, vp, u32, vp, u32, u32, vp],
+        "tl_kv_gather_q8": [ctypes.POINTER(KvLayerQ8), vp, u32, vp, vp, vp, vp, vp],
+        "tl_attn_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs), vp],
+        "tl_attn_noappend_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs), vp],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
@@ -112,6 +123,25 @@ class Layer:
         self.v = torch.zeros_like(self.k)
         self.desc = KvLayer(self.k.data_ptr(), self.v.data_ptr(), cap,
                             n_kv_head, head_dim, ring)
+
+    @property
+    def cap(self):
+        return self.desc.cap
+
+
+class LayerQ8:
+    """One layer of Q8_0 K/V storage (int8 values + f16 scales), allocated by
+    torch: values [n_kv][cap][head_dim] int8, scales [n_kv][cap][head_dim/32]."""
+
+    def __init__(self, cap, n_kv_head, head_dim, ring=0, device="cuda"):
+        import torch
+        self.k = torch.zeros((n_kv_head, cap, head_dim), dtype=torch.int8, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.ks = torch.zeros((n_kv_head, cap, head_dim // 32), dtype=torch.int16,
+                              device=device)
+        self.vs = torch.zeros_like(self.ks)
+        self.desc = KvLayerQ8(self.k.data_ptr(), self.v.data_ptr(), self.ks.data_ptr(),
+                              self.vs.data_ptr(), cap, n_kv_head, head_dim, ring)
 
     @property
     def cap(self):
