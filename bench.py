@@ -53,6 +53,14 @@ def decode_bytes(c, P):
     return P * B + c["Hq"] * c["d"] * 4 * 2 + c["Hkv"] * c["d"] * 2 * (4 + 2)
 
 
+def decode_bytes_q8(c, P):
+    """Algorithmic bytes of one decode OP_ATTN over a Q8_0 cache with P visible
+    keys (rows already appended): int8 K+V rows and their f16 scales (one per
+    32 values) read, q read (f32), out written (f32)."""
+    B = 2 * c["Hkv"] * (c["d"] + c["d"] // 32 * 2)
+    return P * B + c["Hq"] * c["d"] * 4 * 2
+
+
 def prefill_flops(c, p0, n):
     """QK^T + PV flops of one layer's chunk of n rows at positions p0.. (causal)."""
     keys = n * p0 + n * (n + 1) // 2
@@ -385,6 +393,110 @@ def run_config3(torch, tlkv, lib, sh, gen):
                     "planning) between launches; bytes are algorithmic"}
 
 
+def run_q8(torch, tlkv, lib, sh, gen, c, steps):
+    """Config 4 over a Q8_0 cache: the same 64 x 512-row chunks quantized into
+    every layer (tl_kv_append_q8) with chunked-prefill attention over them
+    (tl_attn_noappend_q8, MFMA kernel dequantizing its tiles), then decode
+    steps over the contiguous cache at P = ctx + 1 keys: attention alone
+    (tl_attn_noappend_q8, one launch) and OP_ATTN with the new row
+    (tl_attn_q8: quantizing append + attention, two launches)."""
+    L, Hq, Hkv, d, ub = c["L"], c["Hq"], c["Hkv"], c["d"], c["ub"]
+    kd, qd = Hkv * d, Hq * d
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    stream = torch.cuda.current_stream()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    cap = c["ctx"] + steps + 8
+    layers = [tlkv.LayerQ8(cap, Hkv, d) for _ in range(L)]
+    descs = [x.desc for x in layers]
+    n_chunks = c["ctx"] // ub
+    ck = torch.empty((L, ub, kd), dtype=torch.float32, device="cuda")
+    cv = torch.empty((L, ub, kd), dtype=torch.float32, device="cuda")
+    cq = torch.empty((L, ub, qd), dtype=torch.float32, device="cuda")
+    co = torch.empty((L, ub, qd), dtype=torch.float32, device="cuda")
+    app_ms = pf_ms = 0.0
+    pf_flops = 0
+    e = [ev(), ev(), ev()]
+    for ci in range(n_chunks):
+        p0 = ci * ub
+        ck.normal_(generator=gen)
+        cv.normal_(generator=gen)
+        cq.normal_(generator=gen)
+        e[0].record(stream)
+        for l in range(L):
+            tlkv.check(lib.tl_kv_append_q8(descs[l], tlkv.ptr(ck[l]), tlkv.ptr(cv[l]), kd,
+                                           None, p0, ub, sh))
+        e[1].record(stream)
+        for l in range(L):
+            a = tlkv.attn_args(cq[l], None, None, co[l], None, p0, ub, Hq, d, Hkv, 0, scale)
+            tlkv.check(lib.tl_attn_noappend_q8(descs[l], a, sh))
+        pf_flops += L * prefill_flops(c, p0, ub)
+        e[2].record(stream)
+        torch.cuda.synchronize()
+        app_ms += e[0].elapsed_time(e[1])
+        pf_ms += e[1].elapsed_time(e[2])
+    del ck, cv, cq, co
+    q = torch.randn((L, 1, qd), generator=gen, device="cuda")
+    k = torch.randn((L, 1, kd), generator=gen, device="cuda")
+    v = torch.randn((L, 1, kd), generator=gen, device="cuda")
+    out = torch.empty((L, 1, qd), dtype=torch.float32, device="cuda")
+    P = c["ctx"]
+    a_no = [tlkv.attn_args(q[l], None, None, out[l], None, P, 1, Hq, d, Hkv, 0, scale)
+            for l in range(L)]
+    noapp = lib.tl_attn_noappend_q8
+    # the row at position P (read by the no-append launches)
+    for l in range(L):
+        tlkv.check(lib.tl_kv_append_q8(descs[l], tlkv.ptr(k[l]), tlkv.ptr(v[l]), kd, None,
+                                       P, 1, sh))
+        tlkv.check(noapp(descs[l], a_no[l], sh))
+    torch.cuda.synchronize()
+    n_st = min(128, steps)
+    c0, c1 = ev(), ev()
+    c0.record(stream)
+    for _ in range(n_st):
+        for l in range(L):
+            rc = noapp(descs[l], a_no[l], sh)
+            if rc:
+                tlkv.check(rc)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    us = c0.elapsed_time(c1) * 1e3 / (n_st * L)
+    nbytes = decode_bytes_q8(c, P + 1)
+    f16_bytes = decode_bytes(c, P + 1) - Hkv * d * 2 * 6
+    # OP_ATTN with the new row: quantizing append + attention
+    a_ap = [tlkv.attn_args(q[l], k[l], v[l], out[l], None, P + 1, 1, Hq, d, Hkv, 0, scale)
+            for l in range(L)]
+    attn = lib.tl_attn_q8
+    c2, c3 = ev(), ev()
+    c2.record(stream)
+    for s in range(n_st):
+        for l in range(L):
+            a = a_ap[l]
+            a.pos = P + 1 + s
+            rc = attn(descs[l], a, sh)
+            if rc:
+                tlkv.check(rc)
+    c3.record(stream)
+    torch.cuda.synchronize()
+    us_app = c2.elapsed_time(c3) * 1e3 / (n_st * L)
+    tf = pf_flops / (pf_ms / 1e3) / 1e12
+    del layers
+    return {
+        "decode": {"us_per_layer_launch": round(us, 3),
+                   "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                   "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "f16_equivalent_GBs": round(f16_bytes / (us * 1e-6) / 1e9, 1),
+                   "steps": n_st, "keys": P + 1,
+                   "kernel": "attn_decode_ring_kernel<128,4,false,true>",
+                   "note": "tl_attn_noappend_q8 over the contiguous Q8_0 cache; GBs counts "
+                           "int8 rows + f16 scales, f16_equivalent_GBs the bytes of the same "
+                           "keys in the f16 cache"},
+        "decode_with_append_us_per_layer": round(us_app, 3),
+        "append_tok_s": round(n_chunks * ub / (app_ms / 1e3), 1),
+        "prefill_TFLOPs": round(tf, 2),
+        "prefill_frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -393,6 +505,7 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=96,
                     help="decode-layer calls timed for the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-q8", action="store_true", help="skip the Q8_0-cache rows")
     ap.add_argument("--no-prefill-attn", action="store_true",
                     help="fill the cache with appends only (skips phase 2)")
     ap.add_argument("--ctx", type=int, default=CFG4["ctx"])
@@ -612,7 +725,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(),
-                     "kernel": "attn_decode_ring_kernel<128,4,false> (one OP_ATTN launch, "
+                     "kernel": "attn_decode_ring_kernel<128,4,false,false> (one OP_ATTN launch, "
                                "split merge inside)"},
     }
     if not args.no_prefill_attn:
@@ -622,6 +735,9 @@ def main():
                           "kernel": "attn_prefill_kernel<128,4> (+ split merge)"}
     del layers, slots, q, k, v, out
     torch.cuda.empty_cache()
+    if not args.no_q8:
+        res["q8_0_cache"] = run_q8(torch, tlkv, lib, sh, gen, c, K)
+        torch.cuda.empty_cache()
     others = {}
     runners = {"1": run_config1, "2": run_config2, "3": run_config3, "5": run_config5}
     for cid in [x for x in args.configs.split(",") if x]:

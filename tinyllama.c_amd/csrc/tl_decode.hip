@@ -193,6 +193,14 @@ TL_DEV void lds_dma4(u32 m0, const void *base, u32 voff) {
 
 /* Q8_0 tiles: 6 loads each (K and V values 2 + 2, K and V scales 1 + 1) */
 TL_DEV void wait_tiles_q8(u32 n) {
+#ifdef TL_Q8_NOSCALE
+    switch (n) {
+    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); return;
+    case 1: __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory"); return;
+    case 2: __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory"); return;
+    default: __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory"); return;
+    }
+#endif
     switch (n) {
     case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     case 1: __asm__ volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
@@ -679,10 +687,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             const u32 sph = phys(min(tb + (u32)srow, klast));
             const u32 soff = (sph * (D / 32) + 2 * sw) * 2;
             const u32 ls = scl_lds + (j % S) * 256;
+#ifndef TL_Q8_NOSCALE
             if (lane < 32) {
                 lds_dma4(ls, KS, soff);
                 lds_dma4(ls + 128, VS, soff);
             }
+#endif
             return;
         }
 #pragma unroll
