@@ -85,11 +85,17 @@ typedef struct {
 } KvStateSnapshot;
 
 /* Recurrent-state callbacks (the reference calls graph_state_bytes/save/load,
- * src/graph.c:368-408). */
+ * src/graph.c:368-408).  alloc / release (optional) own the snapshot
+ * storage: when set, a snapshot's `state` comes from alloc(s, bytes) — e.g.
+ * device memory, so save/load are device-to-device copies
+ * (tl_session_set_state) — and is returned with release(s, ptr); when NULL
+ * it is host memory (malloc/free, as the reference's smalloc/sfree). */
 typedef struct {
     size_t (*bytes)(Session *s);
     bool   (*save)(Session *s, void *dst, size_t cap);
     bool   (*load)(Session *s, const void *src, size_t len);
+    void  *(*alloc)(Session *s, size_t bytes);
+    void   (*release)(Session *s, void *ptr);
 } TlKvStateOps;
 
 typedef struct KvRadixCache KvRadixCache;

@@ -8,11 +8,15 @@
  *   tl_session_create     cache_build_attn_kvcache, src/graph.c:817-872
  *                         (per-layer K/V storage sized ctx_size, radix created
  *                         with kv_cache_create(s, kc, ctx_size))
- *   tl_session_kv_prepare graph_kv_prepare, src/graph.c:1423-1454, for the
- *                         stateless (rewindable) architectures: match, reset,
- *                         resume = matched < n ? matched : matched - 1
- *                         (0 when nothing matched); the caller then sets the
+ *   tl_session_kv_prepare graph_kv_prepare, src/graph.c:1423-1454: match,
+ *                         reset, resume = matched < n ? matched : matched - 1
+ *                         (0 when nothing matched) for stateless archs, the
+ *                         snapshot restore for stateful ones
+ *                         (tl_session_set_state); the caller then sets the
  *                         position to `resume` as server.c:834-837 does
+ *   tl_session_set_state / tl_session_checkpoint
+ *                         graph_state registration and graph_kv_checkpoint
+ *                         (src/graph.c:340-408, 1456-1460) with device snapshots
  *   tl_session_execute    graph_execute, src/graph.c:1360-1421, restricted to
  *                         the KV path: n_ubatch chunks, kv_cache_append per
  *                         chunk ("KV slot allocation failed" -> TL_ERANGE),
@@ -86,6 +90,21 @@ int  tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t
  * one launch.  Rows [n_live, ctx_size) are then free as one block.
  * *evicted / *moved (may be NULL) = rows evicted / moved. */
 int  tl_session_compact(tl_session *s, uint32_t keep, uint32_t *evicted, uint32_t *moved);
+
+/* Recurrent state of a stateful arch (hybrid Gated DeltaNet / SSM layers):
+ * register the session's device state buffers (graph_state(),
+ * src/graph.c:340-366; NULL / 0 = stateless).  The prefix cache then keeps
+ * snapshots of them in device memory (kv_cache_checkpoint / restore with
+ * device-to-device copies, tl_state_copy, on the session's stream), and
+ * tl_session_kv_prepare follows graph_kv_prepare's stateful rule
+ * (src/graph.c:1427-1449): a pure continuation keeps the state, anything else
+ * zeroes it and resumes at the deepest restored snapshot (0 when none).
+ * Re-registering drops the existing snapshots. */
+int  tl_session_set_state(tl_session *s, const tl_state_seg *segs, uint32_t n_seg);
+
+/* graph_kv_checkpoint (src/graph.c:1456-1460): snapshot the state at the
+ * current position (no-op without radix or state). */
+int  tl_session_checkpoint(tl_session *s);
 
 /* accessors */
 uint32_t           tl_session_pos(const tl_session *s);        /* Session.n_tokens */

@@ -185,6 +185,26 @@ int tl_rope(float *x, uint32_t rows, uint32_t row_stride, uint32_t heads,
             uint32_t head_dim, uint32_t rope_dim, uint32_t pos, float theta,
             int neox, void *stream);
 
+/* ---- recurrent-state snapshots on the device ------------------------------
+ * graph_state_save / graph_state_load (src/graph.c:368-408) copy every
+ * registered state buffer to / from one host snapshot with a cudaMemcpy per
+ * buffer.  tl_state_copy does the same between device buffers and a device
+ * snapshot in one launch: dir TL_STATE_SAVE concatenates segs[0..n_seg) into
+ * snap (in order, each seg's bytes), TL_STATE_LOAD splits snap back into
+ * them, TL_STATE_ZERO clears the segments (snap unused; the reset a
+ * stateful arch does before a restore, src/graph.c:1443).  Any sizes and
+ * alignments; 16-byte aligned segments move 16 bytes per lane. */
+#define TL_STATE_SAVE 0
+#define TL_STATE_LOAD 1
+#define TL_STATE_ZERO 2
+typedef struct tl_state_seg {
+    void     *ptr;        /* device */
+    uint64_t  bytes;
+} tl_state_seg;
+
+int tl_state_copy(const tl_state_seg *segs, uint32_t n_seg, void *snap, int dir,
+                  void *stream);
+
 /* ---- Q8_0 cache ------------------------------------------------------------
  * A quantized KV cache (the reference's cache is f32, and its notes list a
  * quantized KV cache as missing, REMEMBER.md:18).  Each row of each head is

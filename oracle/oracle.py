@@ -97,6 +97,17 @@ def ref():
         R.rh_kv_stats.argtypes = [_vp, _u64p]
         R.rh_kv_meta.argtypes = [_vp, _u32, _u32p]
         R.rh_dequant_q8_0.argtypes = [_vp, ctypes.c_uint64, _f32p]
+        R.rh_kvs_create.argtypes = [_u32, ctypes.c_uint64]
+        R.rh_kvs_create.restype = _vp
+        R.rh_kvs_destroy.argtypes = [_vp]
+        R.rh_kvs_set_state.argtypes = [_vp, _vp]
+        R.rh_kvs_get_state.argtypes = [_vp, _vp]
+        R.rh_kvs_cap_snaps.argtypes = [_vp]
+        R.rh_kvs_cap_snaps.restype = _u32
+        R.rh_kvs_checkpoint.argtypes = [_vp, _u32]
+        R.rh_kvs_checkpoint.restype = ctypes.c_int
+        R.rh_kvs_restore.argtypes = [_vp, _u32, _u32, _u32p]
+        R.rh_kvs_restore.restype = _u32
         _ref = R
     return _ref
 

@@ -7,6 +7,10 @@
  *   rh_attn      -> cpu_graph_op(OP_ATTN)      src/backend/cpu/cpu_op.c:1070,964
  *   rh_rope      -> cpu_graph_op(OP_ROPE_*)    src/backend/cpu/cpu_op.c:653,674
  *   rh_kv_*      -> kv_cache_create/match/append/destroy  src/kvcache.c:122-270
+ *   rh_kvs_*     -> the same with a Session whose Graph registers one host
+ *                   recurrent-state buffer (graph_state_bytes/save/load,
+ *                   src/graph.c:360-408), and kv_cache_checkpoint/restore
+ *                   src/kvcache.c:272-321
  *   rh_dequant_q8_0 -> gguf_dequant(GGUF_TYPE_Q8_0)  src/quants.c:640-652,368
  *
  * The structs are the reference's own (def.h / kvcache.h); only the fields
@@ -188,4 +192,63 @@ void rh_kv_meta(void *p, u32 slot, u32 *out7) {
     out7[4] = m->in_tree;
     out7[5] = (u32)m->last_used;
     out7[6] = (u32)(m->last_used >> 32);
+}
+
+/* --- kvcache with recurrent state ------------------------------------------ */
+
+typedef struct {
+    RhKv base;                 /* first: the rh_kv_* accessors take it */
+    Session s;
+    Graph g;
+    void *buf[1];
+    size_t size[1];
+    BackendType be[1];
+} RhKvS;
+
+void *rh_kvs_create(u32 ctx, u64 state_bytes) {
+    RhKvS *h = calloc(1, sizeof(*h));
+    h->buf[0] = calloc(1, (size_t)state_bytes);
+    h->size[0] = (size_t)state_bytes;
+    h->be[0] = BACKEND_CPU;
+    h->g.state = h->buf;
+    h->g.state_size = h->size;
+    h->g.state_backend = h->be;
+    h->g.n_state = 1;
+    h->g.state_cap = 1;
+    h->s.graph = &h->g;
+    h->base.kv.n_layer = 1;
+    h->base.c = kv_cache_create(&h->s, &h->base.kv, ctx);
+    if (!h->base.c) { free(h->buf[0]); free(h); return NULL; }
+    return h;
+}
+
+void rh_kvs_destroy(void *p) {
+    RhKvS *h = p;
+    if (!h) return;
+    kv_cache_destroy(h->base.c);
+    free(h->buf[0]);
+    free(h);
+}
+
+void rh_kvs_set_state(void *p, const u8 *src) {
+    RhKvS *h = p;
+    memcpy(h->buf[0], src, h->size[0]);
+}
+
+void rh_kvs_get_state(void *p, u8 *dst) {
+    RhKvS *h = p;
+    memcpy(dst, h->buf[0], h->size[0]);
+}
+
+u32 rh_kvs_cap_snaps(void *p) { return ((RhKvS *)p)->base.c->cap_snaps; }
+
+int rh_kvs_checkpoint(void *p, u32 pos) {
+    return kv_cache_checkpoint(((RhKvS *)p)->base.c, pos) ? 1 : 0;
+}
+
+u32 rh_kvs_restore(void *p, u32 matched, u32 n, u32 *restored) {
+    bool r = false;
+    u32 pos = kv_cache_restore(((RhKvS *)p)->base.c, matched, n, &r);
+    *restored = r ? 1 : 0;
+    return pos;
 }

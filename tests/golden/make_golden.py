@@ -12,6 +12,11 @@ Fixtures (numpy .npz, no pickles):
   op_attn.npz        cpu_graph_op(OP_ATTN) outputs over an f32 cache for tiny
                      GQA / window / slot-table cases (inputs included).
   rope.npz           cpu_graph_op(OP_ROPE_NORM / OP_ROPE_NEOX) outputs.
+  kvcache_state.npz  kv_cache_checkpoint / kv_cache_restore over a Session
+                     with one registered recurrent-state buffer: per request
+                     the match, the restore result (position, flag) and the
+                     state bytes after it, then chunked appends each followed
+                     by a new state pattern and a checkpoint.
   q8_0_dequant.npz   gguf_dequant(GGUF_TYPE_Q8_0) over GGUF Q8_0 blocks with
                      random int8 values (all 256 codes) and binary16 scales
                      (normal, subnormal, zero, negative).
@@ -141,6 +146,93 @@ def gen_rope():
     np.savez_compressed(os.path.join(HERE, "rope.npz"), **arrays)
 
 
+STATE_BYTES = 64
+
+
+def state_pattern(req, pos):
+    """the recurrent state a forward pass would leave at `pos` of request `req`"""
+    return np.random.default_rng(req * 100003 + pos).integers(0, 256, STATE_BYTES).astype(np.uint8)
+
+
+def kvstate_ops(seed=7, ctx=160, n_req=70, vocab=30, chunk=24):
+    """requests sharing prefixes; ops per request: (req, tokens, n_chunks)"""
+    rng = np.random.default_rng(seed)
+    prefixes = [rng.integers(0, vocab, size=rng.integers(4, 60)) for _ in range(5)]
+    reqs = []
+    for r in range(n_req):
+        toks = np.concatenate([prefixes[rng.integers(len(prefixes))],
+                               rng.integers(0, vocab, size=rng.integers(1, 40))])
+        reqs.append(toks[:ctx].astype(np.uint32))
+    return ctx, chunk, reqs
+
+
+def run_kvstate(api):
+    """Drive one implementation (api: match, restore, append, checkpoint,
+    set_state, get_state) through kvstate_ops; returns the per-request log
+    [matched, restore_pos, restored, append_ok...] and the state bytes after
+    each restore."""
+    ctx, chunk, reqs = kvstate_ops()
+    log, states = [], []
+    for r, toks in enumerate(reqs):
+        n = toks.size
+        m = api.match(toks)
+        api.set_state(np.zeros(STATE_BYTES, np.uint8))   # reset before restore
+        pos, restored = api.restore(m, n)
+        states.append(api.get_state())
+        ok = []
+        p = pos
+        while p < n:
+            c = min(chunk, n - p)
+            ok.append(int(api.append(toks, p, c)))
+            if not ok[-1]:
+                break
+            p += c
+            api.set_state(state_pattern(r, p))
+            ok.append(int(api.checkpoint(p)))
+        log.append([m, pos, int(restored), len(ok), sum(ok)])
+    return np.array(log, dtype=np.int64), np.array(states, dtype=np.uint8)
+
+
+class RefStateApi:
+    def __init__(self, ctx):
+        self.R = O.ref()
+        self.h = self.R.rh_kvs_create(ctx, STATE_BYTES)
+
+    def match(self, toks):
+        a = np.ascontiguousarray(toks, dtype=np.uint32)
+        return int(self.R.rh_kv_match(self.h, a, a.size))
+
+    def restore(self, m, n):
+        flag = np.zeros(1, dtype=np.uint32)
+        pos = int(self.R.rh_kvs_restore(self.h, m, n, flag))
+        return pos, bool(flag[0])
+
+    def append(self, toks, pos, n):
+        a = np.ascontiguousarray(toks, dtype=np.uint32)
+        return bool(self.R.rh_kv_append(self.h, a, pos, n))
+
+    def checkpoint(self, pos):
+        return bool(self.R.rh_kvs_checkpoint(self.h, pos))
+
+    def set_state(self, b):
+        b = np.ascontiguousarray(b, dtype=np.uint8)
+        self.R.rh_kvs_set_state(self.h, b.ctypes.data)
+
+    def get_state(self):
+        out = np.zeros(STATE_BYTES, dtype=np.uint8)
+        self.R.rh_kvs_get_state(self.h, out.ctypes.data)
+        return out
+
+
+def gen_kvstate():
+    ctx, _, _ = kvstate_ops()
+    api = RefStateApi(ctx)
+    assert int(api.R.rh_kvs_cap_snaps(api.h)) == 16
+    log, states = run_kvstate(api)
+    api.R.rh_kvs_destroy(api.h)
+    np.savez_compressed(os.path.join(HERE, "kvcache_state.npz"), log=log, states=states)
+
+
 def gen_q8():
     rng = np.random.default_rng(3000)
     nblk = 96
@@ -166,4 +258,5 @@ if __name__ == "__main__":
     gen_attn()
     gen_rope()
     gen_q8()
+    gen_kvstate()
     print("golden vectors written to", HERE)

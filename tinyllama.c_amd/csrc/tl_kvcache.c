@@ -120,6 +120,17 @@ static u32 heap_take(KvRadixCache *c) {
 
 /* ---- snapshots (src/kvcache.c:11-37) ------------------------------------- */
 
+/* snapshot storage: the callbacks' allocator when set, else host memory */
+static void *snap_alloc(KvRadixCache *c) {
+    return c->ops.alloc ? c->ops.alloc(c->s, c->state_bytes) : malloc(c->state_bytes);
+}
+
+static void snap_release(KvRadixCache *c, void *p) {
+    if (!p) return;
+    if (c->ops.release) c->ops.release(c->s, p);
+    else free(p);
+}
+
 static void snapshot_clear(KvRadixCache *c, u32 idx) {
     if (!c->snaps || idx >= c->cap_snaps) return;
     KvStateSnapshot *sn = &c->snaps[idx];
@@ -226,7 +237,7 @@ void kv_cache_destroy(KvRadixCache *c) {
     free(c->cur_key);
     free(c->heap);
     if (c->snaps) {
-        for (u32 i = 0; i < c->cap_snaps; i++) free(c->snaps[i].state);
+        for (u32 i = 0; i < c->cap_snaps; i++) snap_release(c, c->snaps[i].state);
         free(c->snaps);
     }
     free(c);
@@ -271,7 +282,7 @@ void tl_kv_cache_set_state_ops(KvRadixCache *c, const TlKvStateOps *ops) {
     if (c->snaps) {
         for (u32 i = 0; i < c->cap_snaps; i++) {
             snapshot_clear(c, i);
-            free(c->snaps[i].state);
+            snap_release(c, c->snaps[i].state);
         }
         free(c->snaps);
         c->snaps = NULL;
@@ -439,7 +450,7 @@ bool kv_cache_checkpoint(KvRadixCache *c, u32 pos) {
     idx = snapshot_select(c);
     if (idx == KV_SLOT_NONE) return true;
     KvStateSnapshot *sn = &c->snaps[idx];
-    if (!sn->state) sn->state = malloc(c->state_bytes);
+    if (!sn->state) sn->state = snap_alloc(c);
     if (!sn->state || !c->ops.save(c->s, sn->state, c->state_bytes)) return false;
     sn->valid = true;
     sn->slot = slot;

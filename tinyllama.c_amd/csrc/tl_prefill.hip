@@ -264,7 +264,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const u32 key = tb + 32 * kb + 8 * (r / 4) + 4 * h + (r % 4);
-                    sv[kb][r] = (key >= klo) & (key < khi) ? sv[kb][r] : NEG_INF;
+                    sv[kb][r] = ((key >= klo) & (key < khi)) ? sv[kb][r] : NEG_INF;
                 }
         }
         float mt = NEG_INF;

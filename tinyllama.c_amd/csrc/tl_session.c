@@ -29,6 +29,9 @@ struct tl_session {
     uint32_t       stage_pos;
     float          scale;
     int            has_ring;    /* some layer keeps only a window of rows */
+    tl_state_seg  *state;       /* registered recurrent-state buffers (device) */
+    uint32_t       n_state;
+    size_t         state_bytes; /* their total (graph_state_bytes) */
 };
 
 static int fail(int code, const char *msg) { return tl_set_error(code, msg); }
@@ -41,6 +44,7 @@ void tl_session_destroy(tl_session *s) {
     free(s->window);
     kv_cache_destroy(s->radix);
     free(s->tokens);
+    free(s->state);
     if (s->d_slots) (void)hipFree(s->d_slots);
     if (s->d_moves) (void)hipFree(s->d_moves);
     free(s->h_moves);
@@ -82,7 +86,9 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
     }
     if (cfg->use_radix) {
         /* the prefix cache only stores the KvCache pointer */
-        s->radix = kv_cache_create(NULL, (KvCache *)s->layers, cfg->ctx_size);
+        /* the prefix cache only stores the KvCache pointer; the session is
+         * handed back to the state callbacks */
+        s->radix = kv_cache_create((Session *)s, (KvCache *)s->layers, cfg->ctx_size);
         if (!s->radix) {
             tl_session_destroy(s);
             return fail(TL_ENOMEM, "session: kv_cache_create failed");
@@ -155,10 +161,27 @@ int tl_session_kv_prepare(tl_session *s, const uint32_t *tokens, uint32_t n,
         uint32_t limit = s->n_tokens < n ? s->n_tokens : n;
         while (m < limit && s->tokens[m] == tokens[m]) m++;
     }
-    uint32_t r = m == 0 ? 0 : (m < n ? m : m - 1);
-    /* ring layers hold only the last window + n_ubatch - 1 rows of the
-     * previous request: a prefix hit cannot be resumed on them */
-    if (s->has_ring) r = 0;
+    uint32_t r;
+    if (s->state_bytes && m == s->n_tokens && n > m) {
+        /* stateful continuation: keep the state, resume at the match
+         * (src/graph.c:1439-1443) */
+        if (matched) *matched = m;
+        if (resume) *resume = m;
+        return TL_OK;
+    }
+    if (s->state_bytes) {
+        /* reset (zero the state), then restore the deepest snapshot at or
+         * below the match (src/graph.c:1445-1449, kvcache.c:303-321); ring
+         * layers cannot resume, so they take no snapshot either */
+        int rc = tl_state_copy(s->state, s->n_state, NULL, TL_STATE_ZERO, s->cfg.stream);
+        if (rc) return rc;
+        r = (s->radix && !s->has_ring) ? kv_cache_restore(s->radix, m, n, NULL) : 0;
+    } else {
+        r = m == 0 ? 0 : (m < n ? m : m - 1);
+        /* ring layers hold only the last window + n_ubatch - 1 rows of the
+         * previous request: a prefix hit cannot be resumed on them */
+        if (s->has_ring) r = 0;
+    }
     s->n_tokens = r;   /* reset, then resume (src/graph.c:1443-1452, server.c:837) */
     if (r) memcpy(s->tokens, tokens, (size_t)r * sizeof(uint32_t));
     if (matched) *matched = m;
@@ -303,6 +326,73 @@ int tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t 
     if (r) memcpy(s->tokens, tokens, (size_t)r * sizeof(uint32_t));
     if (matched) *matched = m;
     if (resume) *resume = r;
+    return TL_OK;
+}
+
+/* ---- recurrent state (device snapshots) ---------------------------------- */
+
+static size_t state_bytes_cb(Session *ss) { return ((tl_session *)ss)->state_bytes; }
+
+static bool state_save_cb(Session *ss, void *dst, size_t cap) {
+    tl_session *s = (tl_session *)ss;
+    if (cap < s->state_bytes) return false;
+    return tl_state_copy(s->state, s->n_state, dst, TL_STATE_SAVE, s->cfg.stream) == TL_OK;
+}
+
+static bool state_load_cb(Session *ss, const void *src, size_t len) {
+    tl_session *s = (tl_session *)ss;
+    if (len < s->state_bytes) return false;
+    return tl_state_copy(s->state, s->n_state, (void *)src, TL_STATE_LOAD, s->cfg.stream) == TL_OK;
+}
+
+static void *state_alloc_cb(Session *ss, size_t bytes) {
+    (void)ss;
+    void *p = NULL;
+    return hipMalloc(&p, bytes) == hipSuccess ? p : NULL;
+}
+
+static void state_release_cb(Session *ss, void *p) {
+    tl_session *s = (tl_session *)ss;
+    /* a save or load in flight on the session's stream may still use it */
+    (void)hipStreamSynchronize((hipStream_t)s->cfg.stream);
+    (void)hipFree(p);
+}
+
+int tl_session_set_state(tl_session *s, const tl_state_seg *segs, uint32_t n_seg) {
+    if (!s || (n_seg && !segs)) return fail(TL_EINVAL, "set_state: bad arguments");
+    tl_state_seg *copy = NULL;
+    size_t total = 0;
+    if (n_seg) {
+        copy = (tl_state_seg *)malloc((size_t)n_seg * sizeof(*copy));
+        if (!copy) return fail(TL_ENOMEM, "set_state: host allocation");
+        for (uint32_t i = 0; i < n_seg; i++) {
+            if (segs[i].bytes && !segs[i].ptr) {
+                free(copy);
+                return fail(TL_EINVAL, "set_state: null buffer");
+            }
+            copy[i] = segs[i];
+            total += segs[i].bytes;
+        }
+    }
+    /* drop the old snapshots (with the old buffers' callbacks) first */
+    if (s->radix) tl_kv_cache_set_state_ops(s->radix, NULL);
+    free(s->state);
+    s->state = copy;
+    s->n_state = n_seg;
+    s->state_bytes = total;
+    if (s->radix && total) {
+        TlKvStateOps ops = {state_bytes_cb, state_save_cb, state_load_cb, state_alloc_cb,
+                            state_release_cb};
+        tl_kv_cache_set_state_ops(s->radix, &ops);
+    }
+    return TL_OK;
+}
+
+int tl_session_checkpoint(tl_session *s) {
+    if (!s) return fail(TL_EINVAL, "checkpoint: null session");
+    if (!s->radix || !s->state_bytes) return TL_OK;
+    if (!kv_cache_checkpoint(s->radix, s->n_tokens))
+        return fail(TL_ENOMEM, "checkpoint: snapshot allocation or copy failed");
     return TL_OK;
 }
 

@@ -81,6 +81,7 @@ def lib():
         "tl_rope": [vp, u32, u32, u32, u32, u32, u32, ctypes.c_float,
                     ctypes.c_int, vp],
         "tl_probe_read": [vp, ctypes.c_uint64, vp, u32, u32, vp],
+        "tl_state_copy": [ctypes.POINTER(StateSeg), u32, vp, ctypes.c_int, vp],
         "tl_kv_layer_alloc_q8": [ctypes.POINTER(KvLayerQ8), u32, u32, u32, u32],
         "tl_kv_layer_free_q8": [ctypes.POINTER(KvLayerQ8)],
         "tl_kv_append_q8": [ctypes.POINTER(KvLayerQ8), vp, vp, u32, vp, u32, u32, vp],
@@ -176,6 +177,24 @@ class KvRequstStats(ctypes.Structure):
                 ("evictions", ctypes.c_uint64), ("allocations", ctypes.c_uint64)]
 
 
+STATE_BYTES_FN = ctypes.CFUNCTYPE(ctypes.c_size_t, vp)
+STATE_SAVE_FN = ctypes.CFUNCTYPE(ctypes.c_bool, vp, vp, ctypes.c_size_t)
+STATE_LOAD_FN = ctypes.CFUNCTYPE(ctypes.c_bool, vp, vp, ctypes.c_size_t)
+STATE_ALLOC_FN = ctypes.CFUNCTYPE(vp, vp, ctypes.c_size_t)
+STATE_RELEASE_FN = ctypes.CFUNCTYPE(None, vp, vp)
+
+
+class TlKvStateOps(ctypes.Structure):
+    _fields_ = [("bytes", STATE_BYTES_FN), ("save", STATE_SAVE_FN), ("load", STATE_LOAD_FN),
+                ("alloc", STATE_ALLOC_FN), ("release", STATE_RELEASE_FN)]
+
+
+class StateSeg(ctypes.Structure):
+    _fields_ = [("ptr", vp), ("bytes", ctypes.c_uint64)]
+
+
+TL_STATE_SAVE, TL_STATE_LOAD, TL_STATE_ZERO = 0, 1, 2
+
 _kv_sigs_done = False
 
 
@@ -211,6 +230,12 @@ def _kv_sigs():
     L.tl_kv_cache_lookup.restype = u32
     L.tl_kv_cache_trim.argtypes = [vp, u32]
     L.tl_kv_cache_trim.restype = u32
+    L.tl_kv_cache_set_state_ops.argtypes = [vp, ctypes.POINTER(TlKvStateOps)]
+    L.tl_kv_cache_set_state_ops.restype = None
+    L.kv_cache_checkpoint.argtypes = [vp, u32]
+    L.kv_cache_checkpoint.restype = ctypes.c_bool
+    L.kv_cache_restore.argtypes = [vp, u32, u32, ctypes.POINTER(ctypes.c_bool)]
+    L.kv_cache_restore.restype = u32
     _kv_sigs_done = True
     return L
 
@@ -289,6 +314,44 @@ class KvCache:
         """Evict LRU leaves until at most `keep` slots are live; returns evictions."""
         return int(self.L.tl_kv_cache_trim(self.h, keep))
 
+    def set_host_state(self, nbytes):
+        """Install state callbacks over a host buffer of nbytes (self.state, a
+        ctypes array standing for the session's recurrent state); snapshots
+        are host memory.  nbytes = 0 removes them."""
+        if not nbytes:
+            self.L.tl_kv_cache_set_state_ops(self.h, None)
+            self._ops = None
+            return
+        self.state = (ctypes.c_uint8 * nbytes)()
+        st = self.state
+
+        def _bytes(_s):
+            return nbytes
+
+        def _save(_s, dst, cap):
+            if cap < nbytes:
+                return False
+            ctypes.memmove(dst, st, nbytes)
+            return True
+
+        def _load(_s, src, ln):
+            if ln < nbytes:
+                return False
+            ctypes.memmove(st, src, nbytes)
+            return True
+
+        self._ops = TlKvStateOps(STATE_BYTES_FN(_bytes), STATE_SAVE_FN(_save),
+                                 STATE_LOAD_FN(_load), STATE_ALLOC_FN(), STATE_RELEASE_FN())
+        self.L.tl_kv_cache_set_state_ops(self.h, ctypes.byref(self._ops))
+
+    def checkpoint(self, pos):
+        return bool(self.L.kv_cache_checkpoint(self.h, pos))
+
+    def restore(self, matched, n):
+        flag = ctypes.c_bool(False)
+        pos = int(self.L.kv_cache_restore(self.h, matched, n, ctypes.byref(flag)))
+        return pos, bool(flag.value)
+
     def lookup(self, tokens):
         """Read-only longest cached prefix: (length, slots)."""
         import numpy as np
@@ -340,6 +403,10 @@ class Session:
             L.tl_session_append.argtypes = [vp, ctypes.POINTER(u32), u32, ctypes.POINTER(vp),
                                             ctypes.POINTER(vp), u32]
             L.tl_session_append.restype = ctypes.c_int
+            L.tl_session_set_state.argtypes = [vp, ctypes.POINTER(StateSeg), u32]
+            L.tl_session_set_state.restype = ctypes.c_int
+            L.tl_session_checkpoint.argtypes = [vp]
+            L.tl_session_checkpoint.restype = ctypes.c_int
             L._sess_sigs = True
         self.L = L
         self.n_layer = n_layer
@@ -382,6 +449,17 @@ class Session:
     @property
     def radix(self):
         return self.L.tl_session_radix(self.h)
+
+    def set_state(self, tensors):
+        """Register device tensors as the session's recurrent state (they must
+        stay alive while registered); [] = stateless."""
+        segs = (StateSeg * max(len(tensors), 1))(
+            *[StateSeg(t.data_ptr(), t.numel() * t.element_size()) for t in tensors])
+        check(self.L.tl_session_set_state(self.h, segs, len(tensors)))
+        self._state = list(tensors)
+
+    def checkpoint(self):
+        check(self.L.tl_session_checkpoint(self.h))
 
     def append(self, tokens, k, v, kv_stride):
         """K/V write-through only (per-layer device tensors [n_tokens][kv_stride])."""
