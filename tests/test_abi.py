@@ -57,3 +57,25 @@ def test_oracle_loads():
 @pytest.mark.skipif(not O.ref_available(), reason="compiled reference not built")
 def test_reference_harness_loads():
     assert O.ref() is not None
+
+
+def test_argument_errors_need_no_device():
+    """Shape and argument checks run before any HIP call: a rejected layer
+    holds no memory and the calls below return TL_EINVAL without a GPU."""
+    import ctypes
+    lib = tlkv.lib()
+    L8 = tlkv.KvLayerQ8()
+    assert lib.tl_kv_layer_alloc_q8(ctypes.byref(L8), 16, 2, 48, 0) == -1
+    assert not (L8.k or L8.v or L8.ks or L8.vs)
+    assert b"head_dim" in lib.tl_last_error()
+    L = tlkv.KvLayer()
+    assert lib.tl_kv_layer_alloc(ctypes.byref(L), 16, 2, 96, 0) == -1
+    assert not (L.k or L.v)
+    assert lib.tl_kv_layer_alloc(ctypes.byref(L), 16, 2, 64, 17) == -1      # ring > cap
+    a = tlkv.AttnArgs()
+    assert lib.tl_attn_q8(None, ctypes.byref(a), None) == -1
+    assert lib.tl_attn_noappend_q8(ctypes.byref(L8), ctypes.byref(a), None) == -1
+    seg = (tlkv.StateSeg * 1)(tlkv.StateSeg(None, 64))
+    assert lib.tl_state_copy(seg, 1, None, tlkv.TL_STATE_ZERO, None) == -1
+    assert lib.tl_state_copy(seg, 1, None, 7, None) == -1
+    assert lib.tl_state_copy(seg, 0, None, tlkv.TL_STATE_SAVE, None) == 0   # nothing to do

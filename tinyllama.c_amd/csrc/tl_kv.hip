@@ -115,6 +115,12 @@ extern "C" int tl_kv_layer_alloc(tl_kv_layer *L, uint32_t cap, uint32_t n_kv_hea
     memset(L, 0, sizeof(*L));
     size_t bytes = (size_t)cap * n_kv_head * head_dim * sizeof(u16);
     if (bytes == 0) return tl_fail(TL_EINVAL, "empty layer");
+    /* shape rules first, so a rejected layer holds no memory */
+    {
+        tl_kv_layer probe = {(void *)16, (void *)16, cap, n_kv_head, head_dim, ring};
+        int rc = check_layer(&probe);
+        if (rc) return rc;
+    }
     if (hipMalloc(&L->k, bytes) != hipSuccess) {
         L->k = NULL;
         return tl_fail(TL_ENOMEM, "layer K: %zu bytes", bytes);
@@ -125,13 +131,15 @@ extern "C" int tl_kv_layer_alloc(tl_kv_layer *L, uint32_t cap, uint32_t n_kv_hea
         L->v = NULL;
         return tl_fail(TL_ENOMEM, "layer V: %zu bytes", bytes);
     }
-    HIP_TRY(hipMemset(L->k, 0, bytes));
-    HIP_TRY(hipMemset(L->v, 0, bytes));
     L->cap = cap;
     L->n_kv_head = n_kv_head;
     L->head_dim = head_dim;
     L->ring = ring;
-    return check_layer(L);
+    if (hipMemset(L->k, 0, bytes) != hipSuccess || hipMemset(L->v, 0, bytes) != hipSuccess) {
+        tl_kv_layer_free(L);
+        return tl_fail(TL_EHIP, "layer: clearing %zu bytes failed", bytes);
+    }
+    return TL_OK;
 }
 
 extern "C" int tl_kv_layer_free(tl_kv_layer *L) {

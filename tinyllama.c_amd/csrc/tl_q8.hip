@@ -62,10 +62,16 @@ extern "C" int tl_kv_layer_alloc_q8(tl_kv_layer_q8 *L, uint32_t cap, uint32_t n_
                                     uint32_t head_dim, uint32_t ring) {
     if (!L) return tl_fail(TL_EINVAL, "null layer");
     memset(L, 0, sizeof(*L));
-    if (head_dim % 32) return tl_fail(TL_EINVAL, "head_dim %u not a multiple of 32", head_dim);
     const size_t vb = (size_t)cap * n_kv_head * head_dim;
     const size_t sb = vb / 32 * sizeof(u16);
     if (vb == 0) return tl_fail(TL_EINVAL, "empty layer");
+    /* shape rules first, so a rejected layer holds no memory */
+    {
+        tl_kv_layer_q8 probe = {(void *)16, (void *)16, (void *)16, (void *)16,
+                                cap, n_kv_head, head_dim, ring};
+        int rc = check_layer_q8(&probe);
+        if (rc) return rc;
+    }
     void **p[4] = {&L->k, &L->v, &L->ks, &L->vs};
     const size_t bytes[4] = {vb, vb, sb, sb};
     for (int i = 0; i < 4; i++) {
@@ -74,13 +80,16 @@ extern "C" int tl_kv_layer_alloc_q8(tl_kv_layer_q8 *L, uint32_t cap, uint32_t n_
             tl_kv_layer_free_q8(L);
             return tl_fail(TL_ENOMEM, "q8 layer: %zu bytes", bytes[i]);
         }
-        HIP_TRY(hipMemset(*p[i], 0, bytes[i]));
+        if (hipMemset(*p[i], 0, bytes[i]) != hipSuccess) {
+            tl_kv_layer_free_q8(L);
+            return tl_fail(TL_EHIP, "q8 layer: clearing %zu bytes failed", bytes[i]);
+        }
     }
     L->cap = cap;
     L->n_kv_head = n_kv_head;
     L->head_dim = head_dim;
     L->ring = ring;
-    return check_layer_q8(L);
+    return TL_OK;
 }
 
 extern "C" int tl_kv_layer_free_q8(tl_kv_layer_q8 *L) {

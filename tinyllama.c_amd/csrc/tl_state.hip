@@ -48,7 +48,8 @@ __global__ __launch_bounds__(256) void state_copy_kernel(const StateParams p) {
         const u32 s = seg_of(p, b0);
         const u64 in = b0 - p.off[s];
         uint8_t *d = p.seg[s] + in;
-        const bool whole = b0 + 16 <= p.off[s + 1] && ((((uintptr_t)d) | (uintptr_t)(p.snap + b0)) & 15) == 0;
+        const uintptr_t so = p.dir == TL_STATE_ZERO ? 0 : (uintptr_t)(p.snap + b0);
+        const bool whole = b0 + 16 <= p.off[s + 1] && ((((uintptr_t)d) | so) & 15) == 0;
         if (whole) {
             uint4 *sv = (uint4 *)(p.snap + b0);
             if (p.dir == TL_STATE_SAVE) *sv = *(const uint4 *)d;
