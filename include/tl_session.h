@@ -51,6 +51,7 @@ typedef struct tl_session_cfg {
                                      (0 = addressed through the slot table) or NULL */
     int             use_radix;    /* 1: prefix cache maps positions to slots */
     void           *stream;       /* hipStream_t, NULL = default stream */
+    int             kv_q8;        /* 1: Q8_0 cache (tl_kv_layer_q8 storage, tl_attn_q8) */
 } tl_session_cfg;
 
 int  tl_session_create(const tl_session_cfg *cfg, tl_session **out);
@@ -110,7 +111,8 @@ int  tl_session_checkpoint(tl_session *s);
 uint32_t           tl_session_pos(const tl_session *s);        /* Session.n_tokens */
 void               tl_session_set_pos(tl_session *s, uint32_t pos);
 KvRadixCache      *tl_session_radix(tl_session *s);            /* NULL without radix */
-const tl_kv_layer *tl_session_layer(const tl_session *s, uint32_t layer);
+const tl_kv_layer *tl_session_layer(const tl_session *s, uint32_t layer);   /* NULL if kv_q8 */
+const tl_kv_layer_q8 *tl_session_layer_q8(const tl_session *s, uint32_t layer); /* NULL if f16 */
 const uint32_t    *tl_session_device_slots(const tl_session *s);  /* device [ctx_size] */
 
 #ifdef __cplusplus

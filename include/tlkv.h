@@ -248,6 +248,14 @@ int tl_kv_gather_q8(const tl_kv_layer_q8 *L, const uint32_t *slots, uint32_t n,
                     int8_t *k_out, uint16_t *ks_out, int8_t *v_out, uint16_t *vs_out,
                     void *stream);
 
+/* Row copies across layers (prefix fork / compaction, as tl_kv_copy and
+ * tl_kv_copy_between): values and scales of rows src[i] -> dst[i]. */
+int tl_kv_copy_q8(const tl_kv_layer_q8 *layers, uint32_t n_layer, const uint32_t *src,
+                  const uint32_t *dst, uint32_t n, void *stream);
+int tl_kv_copy_between_q8(const tl_kv_layer_q8 *dst_layers, const tl_kv_layer_q8 *src_layers,
+                          uint32_t n_layer, const uint32_t *src, const uint32_t *dst,
+                          uint32_t n, void *stream);
+
 /* OP_ATTN over a Q8_0 cache: quantize-append the batch rows, then attend
  * (decode-sized batches: the split-K kernel reading the int8 rows; larger
  * ones: the MFMA kernel, which dequantizes its K/V tiles to f16 in LDS). */

@@ -17,6 +17,7 @@
  *                        of V each, the block max by DPP within the 8 lanes,
  *                        one 4-byte store of q per lane, lane 0 the scale.
  *   kv_gather_q8_kernel  rows by slot (values and scales).
+ *   kv_copy_q8_kernel    row copies across layers (fork / compaction).
  * Attention: decode-sized batches run the split-K ring kernel's Q8_0
  * instance (tl_decode.hip), larger ones the MFMA prefill kernel, which
  * dequantizes its tiles to f16 as it stages them (tl_prefill.hip).
@@ -255,6 +256,99 @@ extern "C" int tl_kv_gather_q8(const tl_kv_layer_q8 *L, const uint32_t *slots, u
                        ks_out, v_out, vs_out);
     HIP_TRY(hipGetLastError());
     return TL_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* row copies (fork / compaction)                                            */
+/* ------------------------------------------------------------------------ */
+
+#define TL_COPY_Q8_MAX_LAYERS 32
+struct Q8CopyParams {
+    int8_t *k[TL_COPY_Q8_MAX_LAYERS], *v[TL_COPY_Q8_MAX_LAYERS];          /* destination */
+    u16 *ks[TL_COPY_Q8_MAX_LAYERS], *vs[TL_COPY_Q8_MAX_LAYERS];
+    const int8_t *sk[TL_COPY_Q8_MAX_LAYERS], *sv[TL_COPY_Q8_MAX_LAYERS];  /* source */
+    const u16 *sks[TL_COPY_Q8_MAX_LAYERS], *svs[TL_COPY_Q8_MAX_LAYERS];
+    u32 cap, src_cap, n_kv, head_dim;
+};
+
+/* grid: (blocks, layers-in-batch).  One thread per 16 values of K and of V;
+ * the first thread of each 32-value block also moves the two scales. */
+__global__ __launch_bounds__(256) void kv_copy_q8_kernel(const Q8CopyParams p, const u32 *src,
+                                                         const u32 *dst, u32 n) {
+    const u32 l = blockIdx.y;
+    const u32 upr = p.head_dim >> 4;
+    const u64 total = (u64)n * p.n_kv * upr;
+    for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (u64)gridDim.x * blockDim.x) {
+        const u32 c = (u32)(idx % upr);
+        const u64 t = idx / upr;
+        const u32 h = (u32)(t % p.n_kv);
+        const u32 i = (u32)(t / p.n_kv);
+        const u32 s = src[i], d = dst[i];
+        if (s >= p.src_cap || d >= p.cap) continue;
+        const u64 so = ((u64)h * p.src_cap + s) * p.head_dim + c * 16;
+        const u64 dof = ((u64)h * p.cap + d) * p.head_dim + c * 16;
+        *(uint4 *)(p.k[l] + dof) = *(const uint4 *)(p.sk[l] + so);
+        *(uint4 *)(p.v[l] + dof) = *(const uint4 *)(p.sv[l] + so);
+        if ((c & 1) == 0) {
+            p.ks[l][dof / 32] = p.sks[l][so / 32];
+            p.vs[l][dof / 32] = p.svs[l][so / 32];
+        }
+    }
+}
+
+static int copy_rows_q8(const tl_kv_layer_q8 *dl, const tl_kv_layer_q8 *sl, uint32_t n_layer,
+                        const uint32_t *src, const uint32_t *dst, uint32_t n, void *stream) {
+    if (n == 0 || n_layer == 0) return TL_OK;
+    if (!dl || !sl || !src || !dst) return tl_fail(TL_EINVAL, "copy: null pointer");
+    for (u32 l0 = 0; l0 < n_layer; l0 += TL_COPY_Q8_MAX_LAYERS) {
+        const u32 nl = n_layer - l0 < TL_COPY_Q8_MAX_LAYERS ? n_layer - l0 : TL_COPY_Q8_MAX_LAYERS;
+        Q8CopyParams p;
+        memset(&p, 0, sizeof(p));
+        for (u32 j = 0; j < nl; j++) {
+            const tl_kv_layer_q8 *D = &dl[l0 + j], *S = &sl[l0 + j];
+            int rc = check_layer_q8(D);
+            if (!rc) rc = check_layer_q8(S);
+            if (rc) return rc;
+            if (D->ring || S->ring) return tl_fail(TL_EINVAL, "copy: ring layers hold no slot rows");
+            if (j == 0) {
+                p.cap = D->cap;
+                p.src_cap = S->cap;
+                p.n_kv = D->n_kv_head;
+                p.head_dim = D->head_dim;
+            }
+            if (D->cap != p.cap || S->cap != p.src_cap || D->n_kv_head != p.n_kv ||
+                S->n_kv_head != p.n_kv || D->head_dim != p.head_dim || S->head_dim != p.head_dim)
+                return tl_fail(TL_EINVAL, "copy: layers differ in shape");
+            p.k[j] = (int8_t *)D->k;
+            p.v[j] = (int8_t *)D->v;
+            p.ks[j] = (u16 *)D->ks;
+            p.vs[j] = (u16 *)D->vs;
+            p.sk[j] = (const int8_t *)S->k;
+            p.sv[j] = (const int8_t *)S->v;
+            p.sks[j] = (const u16 *)S->ks;
+            p.svs[j] = (const u16 *)S->vs;
+        }
+        const u64 total = (u64)n * p.n_kv * (p.head_dim >> 4);
+        u64 blocks = (total + 255) / 256;
+        if (blocks > 2048) blocks = 2048;
+        hipLaunchKernelGGL(kv_copy_q8_kernel, dim3((u32)blocks, nl), dim3(256), 0,
+                           (hipStream_t)stream, p, src, dst, n);
+        HIP_TRY(hipGetLastError());
+    }
+    return TL_OK;
+}
+
+extern "C" int tl_kv_copy_q8(const tl_kv_layer_q8 *layers, uint32_t n_layer, const uint32_t *src,
+                             const uint32_t *dst, uint32_t n, void *stream) {
+    return copy_rows_q8(layers, layers, n_layer, src, dst, n, stream);
+}
+
+extern "C" int tl_kv_copy_between_q8(const tl_kv_layer_q8 *dst_layers,
+                                     const tl_kv_layer_q8 *src_layers, uint32_t n_layer,
+                                     const uint32_t *src, const uint32_t *dst, uint32_t n,
+                                     void *stream) {
+    return copy_rows_q8(dst_layers, src_layers, n_layer, src, dst, n, stream);
 }
 
 /* ------------------------------------------------------------------------ */

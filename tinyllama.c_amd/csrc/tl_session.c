@@ -18,7 +18,8 @@ int tl_set_error(int code, const char *msg);
 struct tl_session {
     tl_session_cfg cfg;
     uint32_t      *window;      /* [n_layer] */
-    tl_kv_layer   *layers;      /* [n_layer] */
+    tl_kv_layer   *layers;      /* [n_layer] f16 storage, or NULL */
+    tl_kv_layer_q8 *layers8;    /* [n_layer] Q8_0 storage (cfg.kv_q8), or NULL */
     KvRadixCache  *radix;
     uint32_t      *tokens;      /* [ctx_size] host token history (Session.tokens) */
     uint32_t       n_tokens;    /* Session.n_tokens */
@@ -40,7 +41,10 @@ void tl_session_destroy(tl_session *s) {
     if (!s) return;
     if (s->layers)
         for (uint32_t l = 0; l < s->cfg.n_layer; l++) tl_kv_layer_free(&s->layers[l]);
+    if (s->layers8)
+        for (uint32_t l = 0; l < s->cfg.n_layer; l++) tl_kv_layer_free_q8(&s->layers8[l]);
     free(s->layers);
+    free(s->layers8);
     free(s->window);
     kv_cache_destroy(s->radix);
     free(s->tokens);
@@ -63,9 +67,12 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
     s->cfg.window = NULL;
     s->cfg.ring = NULL;
     s->window = (uint32_t *)calloc(cfg->n_layer, sizeof(uint32_t));
-    s->layers = (tl_kv_layer *)calloc(cfg->n_layer, sizeof(tl_kv_layer));
+    if (cfg->kv_q8)
+        s->layers8 = (tl_kv_layer_q8 *)calloc(cfg->n_layer, sizeof(tl_kv_layer_q8));
+    else
+        s->layers = (tl_kv_layer *)calloc(cfg->n_layer, sizeof(tl_kv_layer));
     s->tokens = (uint32_t *)calloc(cfg->ctx_size, sizeof(uint32_t));
-    if (!s->window || !s->layers || !s->tokens) {
+    if (!s->window || (!s->layers && !s->layers8) || !s->tokens) {
         tl_session_destroy(s);
         return fail(TL_ENOMEM, "session: host allocation");
     }
@@ -77,8 +84,10 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
             tl_session_destroy(s);
             return fail(TL_EINVAL, "session: a ring needs window + n_ubatch - 1 rows");
         }
-        int rc = tl_kv_layer_alloc(&s->layers[l], ring ? ring : cfg->ctx_size,
-                                   cfg->n_kv_head, cfg->head_dim, ring);
+        const uint32_t rows = ring ? ring : cfg->ctx_size;
+        int rc = cfg->kv_q8
+                     ? tl_kv_layer_alloc_q8(&s->layers8[l], rows, cfg->n_kv_head, cfg->head_dim, ring)
+                     : tl_kv_layer_alloc(&s->layers[l], rows, cfg->n_kv_head, cfg->head_dim, ring);
         if (rc) {
             tl_session_destroy(s);
             return rc;
@@ -88,7 +97,9 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
         /* the prefix cache only stores the KvCache pointer */
         /* the prefix cache only stores the KvCache pointer; the session is
          * handed back to the state callbacks */
-        s->radix = kv_cache_create((Session *)s, (KvCache *)s->layers, cfg->ctx_size);
+        s->radix = kv_cache_create((Session *)s,
+                                   s->layers8 ? (KvCache *)s->layers8 : (KvCache *)s->layers,
+                                   cfg->ctx_size);
         if (!s->radix) {
             tl_session_destroy(s);
             return fail(TL_ENOMEM, "session: kv_cache_create failed");
@@ -215,9 +226,11 @@ static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
             }
         }
         for (uint32_t l = 0; l < s->cfg.n_layer && !q; l++) {
-            int rc = tl_kv_append(&s->layers[l], k[l] + (size_t)done * kv_stride,
-                                  v[l] + (size_t)done * kv_stride, kv_stride,
-                                  s->radix ? s->d_slots : NULL, p0, chunk, s->cfg.stream);
+            const float *kl = k[l] + (size_t)done * kv_stride, *vl = v[l] + (size_t)done * kv_stride;
+            const uint32_t *sl = s->radix ? s->d_slots : NULL;
+            int rc = s->layers8
+                         ? tl_kv_append_q8(&s->layers8[l], kl, vl, kv_stride, sl, p0, chunk, s->cfg.stream)
+                         : tl_kv_append(&s->layers[l], kl, vl, kv_stride, sl, p0, chunk, s->cfg.stream);
             if (rc) return rc;
         }
         for (uint32_t l = 0; l < s->cfg.n_layer && q; l++) {
@@ -235,7 +248,8 @@ static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
             a.kv_stride = kv_stride;
             a.window = s->window[l];
             a.scale = s->scale;
-            int rc = tl_attn(&s->layers[l], &a, s->cfg.stream);
+            int rc = s->layers8 ? tl_attn_q8(&s->layers8[l], &a, s->cfg.stream)
+                                : tl_attn(&s->layers[l], &a, s->cfg.stream);
             if (rc) return rc;
         }
         done += chunk;
@@ -276,8 +290,11 @@ int tl_session_compact(tl_session *s, uint32_t keep, uint32_t *evicted, uint32_t
     if (n) {
         int rc = upload_words(s, s->d_moves, src, n);
         if (!rc) rc = upload_words(s, s->d_moves + ctx, dst, n);
-        if (!rc) rc = tl_kv_copy(s->layers, s->cfg.n_layer, s->d_moves, s->d_moves + ctx, n,
-                                 s->cfg.stream);
+        if (!rc)
+            rc = s->layers8 ? tl_kv_copy_q8(s->layers8, s->cfg.n_layer, s->d_moves,
+                                            s->d_moves + ctx, n, s->cfg.stream)
+                            : tl_kv_copy(s->layers, s->cfg.n_layer, s->d_moves, s->d_moves + ctx,
+                                         n, s->cfg.stream);
         if (!rc) rc = sync_slots(s);
         if (rc) return rc;
     }
@@ -292,15 +309,17 @@ int tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t 
                                uint32_t n, uint32_t *matched, uint32_t *resume,
                                uint32_t *forked) {
     if (forked) *forked = 0;
-    if (!donor || donor == s || !s || !s->radix || !donor->radix)
+    /* no fork without two prefix caches, or for a stateful session (forked
+     * K/V rows come without the recurrent state at their end) */
+    if (!donor || donor == s || !s || !s->radix || !donor->radix || s->state_bytes)
         return tl_session_kv_prepare(s, tokens, n, matched, resume);
     if (matched) *matched = 0;
     if (resume) *resume = 0;
     if (!tokens || n == 0) return TL_OK;
     if (s->has_ring || donor->has_ring) return fail(TL_EINVAL, "fork: ring layers hold no slot rows");
     if (donor->cfg.n_layer != s->cfg.n_layer || donor->cfg.n_kv_head != s->cfg.n_kv_head ||
-        donor->cfg.head_dim != s->cfg.head_dim)
-        return fail(TL_EINVAL, "fork: sessions differ in shape");
+        donor->cfg.head_dim != s->cfg.head_dim || !donor->layers8 != !s->layers8)
+        return fail(TL_EINVAL, "fork: sessions differ in shape or cache type");
     const uint32_t ctx = s->cfg.ctx_size;
     uint32_t m = kv_cache_match(s->radix, tokens, n);
     uint32_t *src = s->h_moves, *dst = s->h_moves + ctx;
@@ -314,8 +333,11 @@ int tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t 
         memcpy(dst, req->slots + m, (size_t)nc * sizeof(uint32_t));
         int rc = upload_words(s, s->d_moves, src + m, nc);
         if (!rc) rc = upload_words(s, s->d_moves + ctx, dst, nc);
-        if (!rc) rc = tl_kv_copy_between(s->layers, donor->layers, s->cfg.n_layer, s->d_moves,
-                                         s->d_moves + ctx, nc, s->cfg.stream);
+        if (!rc)
+            rc = s->layers8 ? tl_kv_copy_between_q8(s->layers8, donor->layers8, s->cfg.n_layer,
+                                                    s->d_moves, s->d_moves + ctx, nc, s->cfg.stream)
+                            : tl_kv_copy_between(s->layers, donor->layers, s->cfg.n_layer,
+                                                 s->d_moves, s->d_moves + ctx, nc, s->cfg.stream);
         if (!rc) rc = sync_slots(s);
         if (rc) return rc;
         if (forked) *forked = nc;
@@ -401,7 +423,10 @@ void tl_session_set_pos(tl_session *s, uint32_t pos) {
     if (s && pos <= s->cfg.ctx_size) s->n_tokens = pos;
 }
 KvRadixCache *tl_session_radix(tl_session *s) { return s ? s->radix : NULL; }
+const tl_kv_layer_q8 *tl_session_layer_q8(const tl_session *s, uint32_t layer) {
+    return (s && s->layers8 && layer < s->cfg.n_layer) ? &s->layers8[layer] : NULL;
+}
 const tl_kv_layer *tl_session_layer(const tl_session *s, uint32_t layer) {
-    return (s && layer < s->cfg.n_layer) ? &s->layers[layer] : NULL;
+    return (s && s->layers && layer < s->cfg.n_layer) ? &s->layers[layer] : NULL;
 }
 const uint32_t *tl_session_device_slots(const tl_session *s) { return s ? s->d_slots : NULL; }

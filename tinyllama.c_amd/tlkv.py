@@ -86,6 +86,9 @@ def lib():
         "tl_kv_layer_free_q8": [ctypes.POINTER(KvLayerQ8)],
         "tl_kv_append_q8": [ctypes.POINTER(KvLayerQ8), vp, vp, u32, vp, u32, u32, vp],
         "tl_kv_gather_q8": [ctypes.POINTER(KvLayerQ8), vp, u32, vp, vp, vp, vp, vp],
+        "tl_kv_copy_q8": [ctypes.POINTER(KvLayerQ8), u32, vp, vp, u32, vp],
+        "tl_kv_copy_between_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(KvLayerQ8), u32, vp,
+                                  vp, u32, vp],
         "tl_attn_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_noappend_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs), vp],
     }
@@ -367,14 +370,14 @@ class SessionCfg(ctypes.Structure):
     _fields_ = [("n_layer", u32), ("n_head", u32), ("n_kv_head", u32), ("head_dim", u32),
                 ("ctx_size", u32), ("n_ubatch", u32), ("window", ctypes.POINTER(u32)),
                 ("ring", ctypes.POINTER(u32)), ("use_radix", ctypes.c_int),
-                ("stream", vp)]
+                ("stream", vp), ("kv_q8", ctypes.c_int)]
 
 
 class Session:
     """tl_session: device KV storage + host prefix cache + micro-batch loop."""
 
     def __init__(self, n_layer, n_head, n_kv_head, head_dim, ctx_size, n_ubatch,
-                 window=None, ring=None, use_radix=True, stream=None):
+                 window=None, ring=None, use_radix=True, stream=None, kv_q8=False):
         L = lib()
         if not getattr(L, "_sess_sigs", False):
             L.tl_session_create.argtypes = [ctypes.POINTER(SessionCfg), ctypes.POINTER(vp)]
@@ -394,6 +397,8 @@ class Session:
             L.tl_session_radix.restype = vp
             L.tl_session_layer.argtypes = [vp, u32]
             L.tl_session_layer.restype = ctypes.POINTER(KvLayer)
+            L.tl_session_layer_q8.argtypes = [vp, u32]
+            L.tl_session_layer_q8.restype = ctypes.POINTER(KvLayerQ8)
             L.tl_session_kv_prepare_from.argtypes = [vp, vp, ctypes.POINTER(u32), u32,
                                                      ctypes.POINTER(u32), ctypes.POINTER(u32),
                                                      ctypes.POINTER(u32)]
@@ -414,7 +419,7 @@ class Session:
         self._ring = (u32 * n_layer)(*(ring or [0] * n_layer))
         cfg = SessionCfg(n_layer, n_head, n_kv_head, head_dim, ctx_size, n_ubatch,
                          self._win, self._ring, int(use_radix),
-                         None if stream is None else stream)
+                         None if stream is None else stream, int(kv_q8))
         h = vp()
         check(L.tl_session_create(ctypes.byref(cfg), ctypes.byref(h)))
         self.h = h
@@ -486,3 +491,6 @@ class Session:
 
     def layer(self, l):
         return self.L.tl_session_layer(self.h, l).contents
+
+    def layer_q8(self, l):
+        return self.L.tl_session_layer_q8(self.h, l).contents
