@@ -259,12 +259,70 @@ def run_config2(torch, tlkv, lib, sh, gen, steps=512):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
+    del layers, batches
+    keep.clear()
+    torch.cuda.empty_cache()
+    q8 = run_config2_q8(torch, tlkv, lib, sh, gen, q, k, v, out, min(steps, 128))
     return {"workload": f"config 2: L28 Hq28 Hkv4 d128 (gqa 7), 8 sessions x 8192-row cache, "
                         f"{steps} batched decode steps (one launch per layer for all 8)",
+            "q8_0_cache": q8,
             "GBs": round(_gbs(nbytes, ms), 1), "hbm_frac": round(_gbs(nbytes, ms) / HBM_PEAK_GBS, 4),
             "ms_per_step": round(ms / steps, 4),
             "tok_s": round(n_seq * steps / (ms / 1e3), 1),
             "us_per_layer_launch": round(ms * 1e3 / steps / L, 2)}
+
+
+def run_config2_q8(torch, tlkv, lib, sh, gen, q, k, v, out, steps):
+    """Config 2 over Q8_0 caches: the same 8 sessions x 8192 rows (quantized
+    from N(0,1) rows), `steps` batched decode steps of tl_attn_decode_batch_q8
+    (one quantizing append launch + one decode launch per layer)."""
+    L, Hq, Hkv, d, n_seq, P0 = 28, 28, 4, 128, 8, 8192
+    kd = Hkv * d
+    cap = P0 + steps + 8
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    stream = torch.cuda.current_stream()
+    layers = [[tlkv.LayerQ8(cap, Hkv, d) for _ in range(L)] for _ in range(n_seq)]
+    rows = torch.empty((P0, kd), device="cuda")
+    for sl in layers:
+        for lay in sl:
+            rows.normal_(generator=gen)
+            tlkv.check(lib.tl_kv_append_q8(lay.desc, tlkv.ptr(rows), tlkv.ptr(rows), kd, None, 0,
+                                           P0, sh))
+    batches = []
+    for l in range(L):
+        seqs = [tlkv.DecodeSeqQ8(layers[i][l].desc, None, P0, 0, q[i, l].data_ptr(),
+                                 k[i, l].data_ptr(), v[i, l].data_ptr(), out[i, l].data_ptr())
+                for i in range(n_seq)]
+        batches.append((tlkv.DecodeSeqQ8 * n_seq)(*seqs))
+
+    def step(pos):
+        for arr in batches:
+            for i in range(n_seq):
+                arr[i].pos = pos
+            rc = lib.tl_attn_decode_batch_q8(arr, n_seq, Hq, 0, scale, sh)
+            if rc:
+                tlkv.check(rc)
+
+    for w in range(4):
+        step(P0 + w)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    nbytes = 0
+    c = dict(Hq=Hq, Hkv=Hkv, d=d)
+    for s in range(steps):
+        pos = P0 + 4 + s
+        step(pos)
+        nbytes += n_seq * L * decode_bytes_q8(c, pos + 1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    del layers, batches
+    return {"GBs": round(_gbs(nbytes, ms), 1), "steps": steps,
+            "us_per_layer": round(ms * 1e3 / steps / L, 2),
+            "tok_s": round(n_seq * steps / (ms / 1e3), 1),
+            "note": "Q8_0 bytes (int8 rows + f16 scales); per layer one quantizing "
+                    "append launch and one decode launch for the 8 sessions"}
 
 
 def run_config5(torch, tlkv, lib, sh, gen, steps=512):

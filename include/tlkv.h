@@ -248,6 +248,23 @@ int tl_kv_gather_q8(const tl_kv_layer_q8 *L, const uint32_t *slots, uint32_t n,
                     int8_t *k_out, uint16_t *ks_out, int8_t *v_out, uint16_t *vs_out,
                     void *stream);
 
+/* One session of a batched one-token decode over Q8_0 caches. */
+typedef struct tl_decode_seq_q8 {
+    tl_kv_layer_q8  layer;
+    const uint32_t *slots;    /* device slot table of this session, or NULL */
+    uint32_t        pos;      /* position of the new token */
+    uint32_t        pad_;
+    const float    *q;        /* device [n_head*head_dim] f32 */
+    const float    *k;        /* device [n_kv*head_dim] f32 */
+    const float    *v;        /* device [n_kv*head_dim] f32 */
+    float          *dst;      /* device [n_head*head_dim] f32 */
+} tl_decode_seq_q8;
+
+/* tl_attn_decode_batch over Q8_0 caches: one quantizing append launch for
+ * every session's new row, then one decode launch for all sessions. */
+int tl_attn_decode_batch_q8(const tl_decode_seq_q8 *seqs, uint32_t n_seq, uint32_t n_head,
+                            uint32_t window, float scale, void *stream);
+
 /* Row copies across layers (prefix fork / compaction, as tl_kv_copy and
  * tl_kv_copy_between): values and scales of rows src[i] -> dst[i]. */
 int tl_kv_copy_q8(const tl_kv_layer_q8 *layers, uint32_t n_layer, const uint32_t *src,

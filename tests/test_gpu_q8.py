@@ -234,3 +234,49 @@ def test_attn_q8_split_invariance(T):
         assert np.abs(out - ref).max() < TOL, wgs
         outs.append(out)
     assert np.abs(outs[0] - outs[2]).max() < 1e-3
+
+
+@pytest.mark.parametrize("window", [0, 300])
+def test_decode_batch_q8_sessions(T, window):
+    """tl_attn_decode_batch_q8: several sessions (own caches, slot tables or a
+    ring, positions) in one append + one decode launch, each within 2e-3 of
+    the oracle and its new row quantized bit-exactly into its cache."""
+    import tlkv
+    rng = np.random.default_rng(40 + window)
+    n_head, n_kv, hd = 12, 4, 128
+    # cap, pos, permuted slots, ring (a ring needs a window: ring >= window)
+    last = (1100, 2500, False, 1100) if window else (1100, 1093, False, 0)
+    specs = [(1200, 1100, True, 0), (700, 333, False, 0), (2000, 1999, True, 0),
+             (900, 5, True, 0), last]
+    seqs = (tlkv.DecodeSeqQ8 * len(specs))()
+    refs, layers, oc = [], [], []
+    for i, (cap, pos, perm, ring) in enumerate(specs):
+        slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+        hk = rows(rng, pos + 1, n_kv * hd)
+        hv = rows(rng, pos + 1, n_kv * hd)
+        q = rows(rng, 1, n_head * hd)
+        L = tlkv.LayerQ8(cap, n_kv, hd, ring=ring)
+        C = O.CacheQ8(cap, n_kv, hd, ring)
+        ds = None if slots is None else dev(T, slots)
+        lo = max(0, pos - ring) if ring else 0
+        if pos > lo:
+            tlkv.check(tlkv.lib().tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, hk[lo:pos])),
+                                                  tlkv.ptr(dev(T, hv[lo:pos])), n_kv * hd,
+                                                  tlkv.ptr(ds), lo, pos - lo, None))
+            assert C.append(hk[lo:pos], hv[lo:pos], slots, lo, pos - lo) == 0
+        out = T.zeros((1, n_head * hd), dtype=T.float32, device="cuda")
+        seqs[i] = tlkv.DecodeSeqQ8(L.desc, None if ds is None else ds.data_ptr(), pos, 0,
+                                   dev(T, q).data_ptr(), dev(T, hk[pos:]).data_ptr(),
+                                   dev(T, hv[pos:]).data_ptr(), out.data_ptr())
+        refs.append(C.attn(q, hk[pos:], hv[pos:], slots, pos, 1, n_head, window=window))
+        layers.append((L, out))
+        oc.append(C)
+    tlkv.check(tlkv.lib().tl_attn_decode_batch_q8(seqs, len(specs), n_head, window,
+                                                  O.scale_of(hd), None))
+    sync(T)
+    for i, ((L, out), ref, C) in enumerate(zip(layers, refs, oc)):
+        err = np.abs(host(out) - ref).max()
+        assert err < TOL, f"session {i}: {err}"
+        gk, gks, gv, gvs = _q8(L)
+        assert np.array_equal(gk, C.k) and np.array_equal(gks, C.ks), i
+        assert np.array_equal(gv, C.v) and np.array_equal(gvs, C.vs), i

@@ -107,12 +107,16 @@ extern "C" int tl_kv_layer_free_q8(tl_kv_layer_q8 *L) {
 /* quantizing append                                                         */
 /* ------------------------------------------------------------------------ */
 
-struct Q8AppendParams {
+/* one segment: n rows of one layer of one session */
+struct Q8AppendSeg {
     int8_t *k8, *v8;
     u16 *ks, *vs;
     const float *k, *v;
     const u32 *slots;
     u32 cap, ring, n_kv, head_dim, kv_stride, pos, n;
+};
+struct Q8AppendParams {
+    Q8AppendSeg seg[TL_MAX_BATCH_SEQ];
 };
 
 /* 4 values of a block whose scale is 1/id -> 4 int8 in one word */
@@ -127,10 +131,11 @@ TL_DEV float amax4(float4 x) {
     return fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
 }
 
-/* One lane per 4 elements; the 8 lanes of a block are an aligned group of
- * a wave (grid stride and row length are multiples of 8), so the block max
- * is a DPP max within the group. */
-__global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams p) {
+/* grid: (blocks, segments).  One lane per 4 elements; the 8 lanes of a block
+ * are an aligned group of a wave (grid stride and row length are multiples
+ * of 8), so the block max is a DPP max within the group. */
+__global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams pp) {
+    const Q8AppendSeg &p = pp.seg[blockIdx.y];
     const u32 qpr = p.head_dim >> 2;
     const u64 total = (u64)p.n * p.n_kv * qpr;
     for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -160,14 +165,12 @@ __global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams 
     }
 }
 
-static int append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v, u32 kv_stride,
-                     const u32 *slots, u32 pos, u32 n, hipStream_t st) {
-    if (n == 0) return TL_OK;
+static int fill_seg_q8(Q8AppendSeg &p, const tl_kv_layer_q8 *L, const float *k, const float *v,
+                       u32 kv_stride, const u32 *slots, u32 pos, u32 n) {
     if (!k || !v) return tl_fail(TL_EINVAL, "append: null rows");
     if (kv_stride < L->n_kv_head * L->head_dim || (kv_stride & 3) ||
         (((uintptr_t)k | (uintptr_t)v) & 15))
         return tl_fail(TL_EINVAL, "append: rows must be 16-byte aligned, stride %u", kv_stride);
-    Q8AppendParams p;
     p.k8 = (int8_t *)L->k;
     p.v8 = (int8_t *)L->v;
     p.ks = (u16 *)L->ks;
@@ -182,12 +185,31 @@ static int append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v, u3
     p.kv_stride = kv_stride;
     p.pos = pos;
     p.n = n;
-    const u64 total = (u64)n * L->n_kv_head * (L->head_dim / 4);
-    u64 blocks = (total + 255) / 256;
+    return TL_OK;
+}
+
+static int launch_append_q8(const Q8AppendParams &p, u32 n_seg, hipStream_t st) {
+    u64 most = 0;
+    for (u32 i = 0; i < n_seg; i++) {
+        const u64 t = (u64)p.seg[i].n * p.seg[i].n_kv * (p.seg[i].head_dim / 4);
+        if (t > most) most = t;
+    }
+    if (most == 0) return TL_OK;
+    u64 blocks = (most + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(kv_append_q8_kernel, dim3((u32)blocks), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(kv_append_q8_kernel, dim3((u32)blocks, n_seg), dim3(256), 0, st, p);
     HIP_TRY(hipGetLastError());
     return TL_OK;
+}
+
+static int append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v, u32 kv_stride,
+                     const u32 *slots, u32 pos, u32 n, hipStream_t st) {
+    if (n == 0) return TL_OK;
+    Q8AppendParams p;
+    memset(&p, 0, sizeof(p));
+    int rc = fill_seg_q8(p.seg[0], L, k, v, kv_stride, slots, pos, n);
+    if (rc) return rc;
+    return launch_append_q8(p, 1, st);
 }
 
 extern "C" int tl_kv_append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v,
@@ -402,4 +424,59 @@ extern "C" int tl_attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *
 extern "C" int tl_attn_noappend_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a,
                                    void *stream) {
     return attn_q8(L, a, false, (hipStream_t)stream);
+}
+
+extern "C" int tl_attn_decode_batch_q8(const tl_decode_seq_q8 *seqs, uint32_t n_seq,
+                                       uint32_t n_head, uint32_t window, float scale,
+                                       void *stream) {
+    if (n_seq == 0) return TL_OK;
+    if (!seqs || n_seq > TL_MAX_BATCH_SEQ)
+        return tl_fail(TL_EINVAL, "decode_batch: 1..%d sessions", TL_MAX_BATCH_SEQ);
+    const tl_kv_layer_q8 *L0 = &seqs[0].layer;
+    Q8AppendParams ap;
+    memset(&ap, 0, sizeof(ap));
+    DecParams p;
+    memset(&p, 0, sizeof(p));
+    u32 max_vis = 1;
+    for (u32 i = 0; i < n_seq; i++) {
+        const tl_decode_seq_q8 *s = &seqs[i];
+        int rc = check_layer_q8(&s->layer);
+        if (rc) return rc;
+        if (s->layer.n_kv_head != L0->n_kv_head || s->layer.head_dim != L0->head_dim)
+            return tl_fail(TL_EINVAL, "decode_batch: sessions differ in shape");
+        tl_attn_args a;
+        memset(&a, 0, sizeof(a));
+        a.q = s->q; a.k = s->k; a.v = s->v; a.dst = s->dst; a.slots = s->slots;
+        a.pos = s->pos; a.n = 1; a.n_head = n_head;
+        a.q_stride = n_head * s->layer.head_dim;
+        a.kv_stride = s->layer.n_kv_head * s->layer.head_dim;
+        a.window = window; a.scale = scale;
+        rc = tl_check_attn_args(view_q8(&s->layer), &a);
+        if (!rc) rc = fill_seg_q8(ap.seg[i], &s->layer, s->k, s->v, a.kv_stride, s->slots, s->pos, 1);
+        if (rc) return rc;
+        p.seq[i].k = (const u16 *)s->layer.k;
+        p.seq[i].v = (const u16 *)s->layer.v;
+        p.seq[i].ks = (const u16 *)s->layer.ks;
+        p.seq[i].vs = (const u16 *)s->layer.vs;
+        p.seq[i].slots = s->slots;
+        p.seq[i].q = s->q;
+        p.seq[i].dst = s->dst;
+        p.seq[i].cap = s->layer.cap;
+        p.seq[i].ring = s->layer.ring;
+        p.seq[i].pos = s->pos;
+        const u32 nk = s->pos + 1;
+        const u32 vis = (window && nk > window) ? window : nk;
+        if (vis > max_vis) max_vis = vis;
+    }
+    int rc = launch_append_q8(ap, n_seq, (hipStream_t)stream);
+    if (rc) return rc;
+    p.rows_per_seq = 1;
+    p.n_kv = L0->n_kv_head;
+    p.n_head = n_head;
+    p.q_stride = n_head * L0->head_dim;
+    p.window = window;
+    p.scale_log2 = scale * 1.4426950408889634f;
+    tl_rope_cfg(L0->head_dim, nullptr, p.rope);
+    return tl_launch_decode(p, n_seq, L0->head_dim, n_head / L0->n_kv_head, max_vis,
+                            (hipStream_t)stream, true);
 }

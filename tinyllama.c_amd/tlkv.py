@@ -36,6 +36,11 @@ class DecodeSeq(ctypes.Structure):
                 ("q", vp), ("k", vp), ("v", vp), ("dst", vp)]
 
 
+class DecodeSeqQ8(ctypes.Structure):
+    _fields_ = [("layer", KvLayerQ8), ("slots", vp), ("pos", u32), ("pad_", u32),
+                ("q", vp), ("k", vp), ("v", vp), ("dst", vp)]
+
+
 MAX_BATCH_SEQ = 16
 
 
@@ -86,6 +91,8 @@ def lib():
         "tl_kv_layer_free_q8": [ctypes.POINTER(KvLayerQ8)],
         "tl_kv_append_q8": [ctypes.POINTER(KvLayerQ8), vp, vp, u32, vp, u32, u32, vp],
         "tl_kv_gather_q8": [ctypes.POINTER(KvLayerQ8), vp, u32, vp, vp, vp, vp, vp],
+        "tl_attn_decode_batch_q8": [ctypes.POINTER(DecodeSeqQ8), u32, u32, u32, ctypes.c_float,
+                                    vp],
         "tl_kv_copy_q8": [ctypes.POINTER(KvLayerQ8), u32, vp, vp, u32, vp],
         "tl_kv_copy_between_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(KvLayerQ8), u32, vp,
                                   vp, u32, vp],
