@@ -79,3 +79,24 @@ def test_argument_errors_need_no_device():
     assert lib.tl_state_copy(seg, 1, None, tlkv.TL_STATE_ZERO, None) == -1
     assert lib.tl_state_copy(seg, 1, None, 7, None) == -1
     assert lib.tl_state_copy(seg, 0, None, tlkv.TL_STATE_SAVE, None) == 0   # nothing to do
+
+
+def test_size_limits_and_empty_batches_need_no_device():
+    """A kv-head's rows are addressed with 32-bit byte offsets: layers past
+    4 GiB per kv-head are refused before allocating; empty batches are
+    no-ops (no launch)."""
+    import ctypes
+    lib = tlkv.lib()
+    TL_ERANGE = -2
+    L = tlkv.KvLayer()
+    assert lib.tl_kv_layer_alloc(ctypes.byref(L), 1 << 24, 1, 256, 0) == TL_ERANGE
+    assert not (L.k or L.v)
+    L8 = tlkv.KvLayerQ8()
+    assert lib.tl_kv_layer_alloc_q8(ctypes.byref(L8), 1 << 26, 1, 128, 0) == TL_ERANGE
+    assert not (L8.k or L8.ks)
+    # empty batches return before touching the device (storage pointers are fake)
+    fake = tlkv.KvLayerQ8(16, 16, 16, 16, 64, 2, 64, 0)
+    assert lib.tl_kv_append_q8(ctypes.byref(fake), None, None, 128, None, 0, 0, None) == 0
+    a = tlkv.AttnArgs(16, 0, 0, 16, 0, 0, 0, 4, 256, 128, 0, 0.125)
+    assert lib.tl_attn_noappend_q8(ctypes.byref(fake), ctypes.byref(a), None) == 0
+    assert lib.tl_attn_decode_batch_q8(None, 0, 4, 0, 0.125, None) == 0
