@@ -13,6 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libtlref.so")
+SHIM_SO = os.path.join(HERE, "_ref", "libtlshim.so")
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
@@ -110,6 +111,26 @@ def ref():
         R.rh_kvs_restore.restype = _u32
         _ref = R
     return _ref
+
+
+_shim = None
+
+
+def shim_available():
+    return os.path.exists(SHIM_SO)
+
+
+def shim():
+    """The executor shim (tinyllama.c_amd/integration/hip_graph_op.c) with its
+    harness, built against the reference's headers, or None."""
+    global _shim
+    if _shim is None and os.path.exists(SHIM_SO):
+        S = ctypes.CDLL(SHIM_SO)
+        S.rh_attn_shim.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _u32, _u32,
+                                   _u32, _u32, _u32, _u32, _vp]
+        S.rh_attn_shim.restype = ctypes.c_int
+        _shim = S
+    return _shim
 
 
 def scale_of(head_dim):

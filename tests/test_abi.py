@@ -100,3 +100,10 @@ def test_size_limits_and_empty_batches_need_no_device():
     a = tlkv.AttnArgs(16, 0, 0, 16, 0, 0, 0, 4, 256, 128, 0, 0.125)
     assert lib.tl_attn_noappend_q8(ctypes.byref(fake), ctypes.byref(a), None) == 0
     assert lib.tl_attn_decode_batch_q8(None, 0, 4, 0, 0.125, None) == 0
+
+
+@pytest.mark.skipif(not O.shim_available(), reason="executor shim not built (no reference tree)")
+def test_executor_shim_loads():
+    S = O.shim()
+    for name in ("hip_graph_op", "hip_graph_op_set_slots", "hip_graph_op_set_stream"):
+        assert hasattr(S, name)
