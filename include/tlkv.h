@@ -153,6 +153,16 @@ int tl_kv_copy_between(const tl_kv_layer *dst_layers, const tl_kv_layer *src_lay
 int tl_attn_rope(const tl_kv_layer *L, const tl_attn_args *a, const tl_rope_params *rope,
                  void *stream);
 
+/* The write-through of one token batch into several layers in one launch
+ * per 16 layers (no reference counterpart: the reference writes a layer's
+ * rows inside that layer's OP_ATTN, cpu_op.c:995-1008).  For callers that
+ * hold every layer's rows at once — restoring or extending a cache without
+ * attention (tl_session_append).  Layer l takes k[l], v[l]; all layers share
+ * kv_stride, slots, pos and n.  Same bytes as n_layer tl_kv_append calls. */
+int tl_kv_append_layers(const tl_kv_layer *layers, uint32_t n_layer, const float *const *k,
+                        const float *const *v, uint32_t kv_stride, const uint32_t *slots,
+                        uint32_t pos, uint32_t n, void *stream);
+
 /* tl_kv_append with RoPE applied to K on the way (same bits as tl_rope then
  * tl_kv_append; k is not modified). */
 int tl_kv_append_rope(const tl_kv_layer *L, const float *k, const float *v,
@@ -240,6 +250,12 @@ int tl_kv_layer_free_q8(tl_kv_layer_q8 *L);
 int tl_kv_append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v,
                     uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
                     uint32_t n, void *stream);
+
+/* tl_kv_append_layers over Q8_0 layers (same bytes as per-layer
+ * tl_kv_append_q8 calls). */
+int tl_kv_append_layers_q8(const tl_kv_layer_q8 *layers, uint32_t n_layer,
+                           const float *const *k, const float *const *v, uint32_t kv_stride,
+                           const uint32_t *slots, uint32_t pos, uint32_t n, void *stream);
 
 /* Read rows slots[i] of every head: values to k_out/v_out
  * [n][n_kv_head][head_dim] int8, scales to ks_out/vs_out

@@ -447,3 +447,35 @@ def test_decode_deterministic_across_launches(T):
         sync(T)
         outs.append(host(out))
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_append_layers_equals_per_layer(T, q8):
+    """tl_kv_append_layers(_q8): 20 layers (two launches of up to 16) write
+    the same bytes as 20 per-layer appends."""
+    import ctypes
+    import tlkv
+    rng = np.random.default_rng(77 + q8)
+    n_layer, n_kv, hd, cap, pos, n = 20, 4, 128, 300, 17, 45
+    slots = rng.permutation(cap).astype(np.uint32)
+    ds = dev(T, slots)
+    ks = [dev(T, rows(rng, n, n_kv * hd)) for _ in range(n_layer)]
+    vs = [dev(T, rows(rng, n, n_kv * hd)) for _ in range(n_layer)]
+    mk = (lambda: tlkv.LayerQ8(cap, n_kv, hd)) if q8 else (lambda: tlkv.Layer(cap, n_kv, hd))
+    A = [mk() for _ in range(n_layer)]
+    B = [mk() for _ in range(n_layer)]
+    one = tlkv.lib().tl_kv_append_q8 if q8 else tlkv.lib().tl_kv_append
+    for l in range(n_layer):
+        tlkv.check(one(A[l].desc, tlkv.ptr(ks[l]), tlkv.ptr(vs[l]), n_kv * hd, tlkv.ptr(ds),
+                       pos, n, None))
+    Desc = tlkv.KvLayerQ8 if q8 else tlkv.KvLayer
+    descs = (Desc * n_layer)(*[b.desc for b in B])
+    karr = (ctypes.c_void_p * n_layer)(*[t.data_ptr() for t in ks])
+    varr = (ctypes.c_void_p * n_layer)(*[t.data_ptr() for t in vs])
+    many = tlkv.lib().tl_kv_append_layers_q8 if q8 else tlkv.lib().tl_kv_append_layers
+    tlkv.check(many(descs, n_layer, karr, varr, n_kv * hd, tlkv.ptr(ds), pos, n, None))
+    sync(T)
+    for a, b in zip(A, B):
+        assert T.equal(a.k, b.k) and T.equal(a.v, b.v)
+        if q8:
+            assert T.equal(a.ks, b.ks) and T.equal(a.vs, b.vs)

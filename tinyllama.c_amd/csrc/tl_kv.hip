@@ -263,6 +263,28 @@ int tl_rope_cfg(uint32_t head_dim, const tl_rope_params *r, RopeCfg &c) {
     return TL_OK;
 }
 
+extern "C" int tl_kv_append_layers(const tl_kv_layer *layers, uint32_t n_layer,
+                                   const float *const *k, const float *const *v,
+                                   uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                                   uint32_t n, void *stream) {
+    if (n == 0 || n_layer == 0) return TL_OK;
+    if (!layers || !k || !v) return tl_fail(TL_EINVAL, "append_layers: null pointer");
+    for (u32 l0 = 0; l0 < n_layer; l0 += TL_MAX_BATCH_SEQ) {
+        const u32 nl = n_layer - l0 < TL_MAX_BATCH_SEQ ? n_layer - l0 : TL_MAX_BATCH_SEQ;
+        AppendParams p;
+        memset(&p, 0, sizeof(p));
+        for (u32 j = 0; j < nl; j++) {
+            const tl_kv_layer *L = &layers[l0 + j];
+            int rc = check_layer(L);
+            if (!rc) rc = fill_seg(p.seg[j], L, k[l0 + j], v[l0 + j], kv_stride, slots, pos, n);
+            if (rc) return rc;
+        }
+        int rc = tl_launch_append(p, nl, (hipStream_t)stream);
+        if (rc) return rc;
+    }
+    return TL_OK;
+}
+
 static int rope_cfg(const tl_kv_layer *L, const tl_rope_params *r, RopeCfg &c) {
     return tl_rope_cfg(L->head_dim, r, c);
 }

@@ -225,13 +225,24 @@ static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                 if (rc) return rc;
             }
         }
-        for (uint32_t l = 0; l < s->cfg.n_layer && !q; l++) {
-            const float *kl = k[l] + (size_t)done * kv_stride, *vl = v[l] + (size_t)done * kv_stride;
+        if (!q) {
+            /* write-through only: every layer's rows of the chunk, batched
+             * into one launch per 16 layers */
+            const float *kl[64], *vl[64];
             const uint32_t *sl = s->radix ? s->d_slots : NULL;
-            int rc = s->layers8
-                         ? tl_kv_append_q8(&s->layers8[l], kl, vl, kv_stride, sl, p0, chunk, s->cfg.stream)
-                         : tl_kv_append(&s->layers[l], kl, vl, kv_stride, sl, p0, chunk, s->cfg.stream);
-            if (rc) return rc;
+            for (uint32_t l0 = 0; l0 < s->cfg.n_layer; l0 += 64) {
+                const uint32_t nl = s->cfg.n_layer - l0 < 64 ? s->cfg.n_layer - l0 : 64;
+                for (uint32_t j = 0; j < nl; j++) {
+                    kl[j] = k[l0 + j] + (size_t)done * kv_stride;
+                    vl[j] = v[l0 + j] + (size_t)done * kv_stride;
+                }
+                int rc = s->layers8
+                             ? tl_kv_append_layers_q8(&s->layers8[l0], nl, kl, vl, kv_stride, sl,
+                                                      p0, chunk, s->cfg.stream)
+                             : tl_kv_append_layers(&s->layers[l0], nl, kl, vl, kv_stride, sl, p0,
+                                                   chunk, s->cfg.stream);
+                if (rc) return rc;
+            }
         }
         for (uint32_t l = 0; l < s->cfg.n_layer && q; l++) {
             tl_attn_args a;
