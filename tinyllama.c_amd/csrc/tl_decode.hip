@@ -1,5 +1,6 @@
 /*
- * tl_decode.hip — split-K decode attention over the slot-indexed f16 cache.
+ * tl_decode.hip — split-K decode attention over the slot-indexed f16 or
+ * Q8_0 cache.
  *
  * Math of op_attn (reference src/backend/cpu/cpu_op.c:1011-1062): for each
  * q-head h and batch row r, n_keys = pos + r + 1, visible keys
@@ -28,6 +29,11 @@
  *   The fused append of decode rows: the split-0 workgroup of row 0 writes
  *   the new K/V rows; workgroups that need a new key convert it from the f32
  *   input into LDS.
+ *   Q8_0 instance (Q8): int8 rows and their f16 block scales stream through
+ *   a 4-stage ring in the same LDS (values as loaded, scales by 32-lane
+ *   dword loads); int8 -> f16 by byte permutes (exact), scores scaled per
+ *   key block in f32, V dequantized to f16 for the PV v_dot2 (ring_tile_q8);
+ *   no fused append (the quantizing append is its own launch).
  */
 #include "tl_common.h"
 #include "tl_internal.h"

@@ -11,7 +11,9 @@
  *   split-K ("flash-decoding") attention over the slot table, one workgroup
  *   per (split, kv-head, row) serving all q-heads of the GQA group; math of
  *   cpu_op.c:1011-1062.
- * The MFMA chunked-prefill kernel lives in tl_prefill.hip.
+ * The MFMA chunked-prefill kernel lives in tl_prefill.hip, the Q8_0 cache's
+ * storage / append / gather / copies in tl_q8.hip, the recurrent-state
+ * snapshot copies in tl_state.hip.
  */
 #include "tl_common.h"
 #include "tl_internal.h"
