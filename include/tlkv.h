@@ -229,8 +229,7 @@ int tl_state_copy(const tl_state_seg *segs, uint32_t n_seg, void *snap, int dir,
  * q_j = rint(x_j * (d > 0 ? 1/d : 0)) (ties to even), d stored RNE as
  * binary16.  Inputs are expected finite.  Attention over a Q8_0 cache
  * equals attention over the dequantized values q * d.  No counterpart in
- * the reference's KV API (an added format); RoPE is not fused on this path
- * (apply tl_rope to q and k first). */
+ * the reference's KV API (an added format). */
 typedef struct tl_kv_layer_q8 {
     void     *k;          /* device, int8 [n_kv_head][cap][head_dim] */
     void     *v;
@@ -294,6 +293,15 @@ int tl_kv_copy_between_q8(const tl_kv_layer_q8 *dst_layers, const tl_kv_layer_q8
  * ones: the MFMA kernel, which dequantizes its K/V tiles to f16 in LDS). */
 int tl_attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *stream);
 int tl_attn_noappend_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *stream);
+
+/* Fused RoPE over a Q8_0 cache (as tl_attn_rope / tl_kv_append_rope): K is
+ * rotated before it is quantized, q as it is staged; the same bits as
+ * tl_rope on q and k followed by tl_attn_q8 / tl_kv_append_q8. */
+int tl_attn_rope_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a,
+                    const tl_rope_params *rope, void *stream);
+int tl_kv_append_rope_q8(const tl_kv_layer_q8 *L, const float *k, const float *v,
+                         uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                         uint32_t n, const tl_rope_params *rope, void *stream);
 
 /* Measurement aid (no reference counterpart): stream `bytes` of device
  * memory with 16-byte loads, `depth` (1/4/8/16) in flight per lane, over

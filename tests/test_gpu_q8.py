@@ -280,3 +280,43 @@ def test_decode_batch_q8_sessions(T, window):
         gk, gks, gv, gvs = _q8(L)
         assert np.array_equal(gk, C.k) and np.array_equal(gks, C.ks), i
         assert np.array_equal(gv, C.v) and np.array_equal(gvs, C.vs), i
+
+
+@pytest.mark.parametrize("neox,rdim,n,window", [(0, 128, 1, 0), (1, 128, 3, 0), (1, 64, 40, 0),
+                                                 (0, 128, 24, 100), (1, 128, 1, 200)])
+def test_attn_rope_q8_equals_rope_then_attn(T, neox, rdim, n, window):
+    """tl_attn_rope_q8 (K rotated before quantizing, q while staged) gives the
+    same bits as tl_rope on q and k followed by tl_attn_q8: outputs, values
+    and scales."""
+    import tlkv
+    rng = np.random.default_rng(90 + n + neox)
+    n_head, n_kv, hd, cap, pos = 16, 4, 128, 600, 300
+    theta = 10000.0 if neox else 500000.0
+    slots = rng.permutation(cap).astype(np.uint32)
+    hk, hv = rows(rng, pos, n_kv * hd), rows(rng, pos, n_kv * hd)
+    q, k, v = rows(rng, n, n_head * hd), rows(rng, n, n_kv * hd), rows(rng, n, n_kv * hd)
+    rp = tlkv.RopeParams(rdim, theta, neox)
+    outs, lays = [], []
+    for fused in (False, True):
+        L = tlkv.LayerQ8(cap, n_kv, hd)
+        ds = dev(T, slots)
+        tlkv.check(tlkv.lib().tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, hk)), tlkv.ptr(dev(T, hv)),
+                                              n_kv * hd, tlkv.ptr(ds), 0, pos, None))
+        dq, dk, dv = dev(T, q), dev(T, k), dev(T, v)
+        out = T.zeros((n, n_head * hd), dtype=T.float32, device="cuda")
+        a = tlkv.attn_args(dq, dk, dv, out, ds, pos, n, n_head, hd, n_kv, window, O.scale_of(hd))
+        if fused:
+            tlkv.check(tlkv.lib().tl_attn_rope_q8(L.desc, a, rp, None))
+        else:
+            lib = tlkv.lib()
+            tlkv.check(lib.tl_rope(tlkv.ptr(dq), n, n_head * hd, n_head, hd, rdim, pos, theta,
+                                   neox, None))
+            tlkv.check(lib.tl_rope(tlkv.ptr(dk), n, n_kv * hd, n_kv, hd, rdim, pos, theta,
+                                   neox, None))
+            tlkv.check(lib.tl_attn_q8(L.desc, a, None))
+        sync(T)
+        outs.append(host(out))
+        lays.append(_q8(L))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for x, y in zip(lays[0], lays[1]):
+        assert np.array_equal(x, y)

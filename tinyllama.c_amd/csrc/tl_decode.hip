@@ -35,918 +35,15 @@
  *   key block in f32, V dequantized to f16 for the PV v_dot2 (ring_tile_q8);
  *   no fused append (the quantizing append is its own launch).
  */
-#include "tl_common.h"
-#include "tl_internal.h"
-
-#include <stdlib.h>
-#include <string.h>
-#include <type_traits>
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-TL_DEV half2_t as_h2(u32 w) { return __builtin_bit_cast(half2_t, w); }
-
-/* 8 f32 -> 8 binary16 (RNE, NaN pinned), the append conversion */
-TL_DEV uint4 cvt8_f16(const float *src) {
-    const float4 a = *(const float4 *)src;
-    const float4 b = *(const float4 *)(src + 4);
-    return make_uint4(pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
-                      pack_f16x2(b.z, b.w));
-}
-
-TL_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-typedef u32 u32x4_t __attribute__((ext_vector_type(4)));
-
-/* 16-byte streaming load (non-temporal: the cache is read once per step). */
-TL_DEV uint4 ld_stream(const u16 *ptr) {
-    u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)ptr);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-TL_DEV u32 perm_lo(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
-TL_DEV u32 perm_hi(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
-
-/* the buffer builtins take and return GCC vectors; read their elements with
- * v[i] into scalars (this compiler mis-reads __builtin_bit_cast of a vector
- * element) */
-typedef u32 u32x4v_t __attribute__((vector_size(16)));
-typedef u32 u32x2v_t __attribute__((vector_size(8)));
-
-/* Raw buffer resource over `base` (offsets are bytes from base). */
-TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7ffffff0, 0x00020000);
-}
-/* Cache policy sc1: device-coherent access (written through to / read from
- * the level every XCD sees), the policy of agent-scope atomics. */
-#define TL_SC1 16
-
-/* Optional per-workgroup timeline (measurement builds only, -DTL_DEC_TRACE):
- * 16 u64 per workgroup: s_memrealtime (100 MHz) at launch entry (0),
- * stream start (1), stream end (2), partial written (3), merge end (4),
- * first tile in (5), epilogue LDS done (8), merge: counter seen (9),
- * partials loaded (10); the XCC (6) and HW (7) ids. */
-#ifdef TL_DEC_TRACE
-__device__ u64 tl_dec_trace[8192 * 16];
-#define TL_TRACE(i)                                                                    \
-    do {                                                                               \
-        if (threadIdx.x == 0 && blockIdx.x < 8192)                                     \
-            tl_dec_trace[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime();      \
-    } while (0)
-#define TL_TRACE_IDS()                                                                 \
-    do {                                                                               \
-        if (threadIdx.x == 0 && blockIdx.x < 8192) {                                   \
-            tl_dec_trace[blockIdx.x * 16 + 6] = __builtin_amdgcn_s_getreg((3 << 11) | 20); \
-            tl_dec_trace[blockIdx.x * 16 + 7] = __builtin_amdgcn_s_getreg((31 << 11) | 4); \
-        }                                                                              \
-    } while (0)
-extern "C" int tl_dec_trace_read(void *host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_dec_trace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#else
-#define TL_TRACE(i) do {} while (0)
-#define TL_TRACE_IDS() do {} while (0)
-#endif
-
-/* Split merge as its own launch (prefill key splits, and decode splits whose
- * partials exceed the in-launch merge).  D/4 threads per output row of one
- * head, each owning a float4: it folds the n_split partials of its float4
- * with an online max, in batches of 8 (all loads of a batch requested
- * together): out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s.
- * grid = ceil(rows * n_head * D/4 / 256), no LDS, no barriers. */
-#define TL_MERGE_MAX_SPLIT 1024
-template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p, u32 n_out) {
-    constexpr float NEG_INF = -__builtin_huge_valf();
-    constexpr int C4 = D / 4;
-    constexpr int K = 8;
-    const u32 gid = blockIdx.x * 256 + threadIdx.x;
-    const u32 o = gid / C4;                       /* (row, head) */
-    if (o >= n_out) return;
-    const u32 d = (gid % C4) * 4;
-    const u32 hq = o % p.n_head, grow = o / p.n_head;
-    const u32 si = grow / p.rows_per_seq, r = grow % p.rows_per_seq;
-    const u32 ns = p.n_split;
-    const u64 pb = (u64)o * ns;
-    float M = NEG_INF, L = 0.f;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (u32 s0 = 0; s0 < ns; s0 += K) {
-        float2 ml[K];
-        float4 a[K];
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-            const u32 s = min(s0 + k, ns - 1);
-            ml[k] = p.ws_ml[pb + s];
-            a[k] = *(const float4 *)&p.ws_acc[(pb + s) * D + d];
-        }
-        float bm = NEG_INF;
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-            if (s0 + k >= ns) ml[k] = make_float2(NEG_INF, 0.f);
-            bm = fmaxf(bm, ml[k].x);
-        }
-        const float nm = fmaxf(M, bm);
-        const float mu = (nm == NEG_INF) ? 0.f : nm;
-        const float sc = fast_exp2(M - mu);
-        L *= sc;
-        O.x *= sc; O.y *= sc; O.z *= sc; O.w *= sc;
-        M = nm;
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-            const float w = fast_exp2(ml[k].x - mu);
-            L = fmaf(w, ml[k].y, L);
-            O.x = fmaf(w, a[k].x, O.x);
-            O.y = fmaf(w, a[k].y, O.y);
-            O.z = fmaf(w, a[k].z, O.z);
-            O.w = fmaf(w, a[k].w, O.w);
-        }
-    }
-    const float inv = 1.0f / L;
-    *(float4 *)&p.seq[si].dst[(u64)r * p.q_stride + (u64)hq * D + d] =
-        make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
-}
-
-/* ------------------------------------------------------------------------ */
-/* Decode attention, LDS-direct ring                                        */
-/* ------------------------------------------------------------------------ */
-
-/* One 16-byte-per-lane load straight into LDS (global_load_lds_dwordx4,
- * non-temporal: the cache is streamed once per step): lane i's 16 bytes land
- * at LDS byte address m0 + 16*i.  Issued from inline
- * assembly so the compiler does not wait for it before every LDS read; the
- * caller waits with an explicit vmcnt.  `base` must be wave-uniform. */
-TL_DEV void lds_dma16(u32 m0, const void *base, u32 voff) {
-    const u64 g = (u64)base;
-    const u32 lo = __builtin_amdgcn_readfirstlane((u32)g);
-    const u32 hi = __builtin_amdgcn_readfirstlane((u32)(g >> 32));
-    const void *sb = (const void *)(((u64)hi << 32) | lo);
-    /* m0 is an input operand (the compiler writes it); s_nop covers the
-     * one-wait-state hazard between an M0 write and an LDS-direct load */
-    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
-                     :: "v"(voff), "s"(sb), "{m0}"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
-}
-
-/* One 4-byte-per-lane load straight into LDS (global_load_lds_dword):
- * lane i's word lands at m0 + 4*i; otherwise as lds_dma16. */
-TL_DEV void lds_dma4(u32 m0, const void *base, u32 voff) {
-    const u64 g = (u64)base;
-    const u32 lo = __builtin_amdgcn_readfirstlane((u32)g);
-    const u32 hi = __builtin_amdgcn_readfirstlane((u32)(g >> 32));
-    const void *sb = (const void *)(((u64)hi << 32) | lo);
-    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1 nt"
-                     :: "v"(voff), "s"(sb), "{m0}"(__builtin_amdgcn_readfirstlane(m0)) : "memory");
-}
-
-/* Q8_0 tiles: 6 loads each (K and V values 2 + 2, K and V scales 1 + 1) */
-TL_DEV void wait_tiles_q8(u32 n) {
-#ifdef TL_Q8_NOSCALE
-    switch (n) {
-    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); return;
-    case 1: __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory"); return;
-    case 2: __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory"); return;
-    default: __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory"); return;
-    }
-#endif
-    switch (n) {
-    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: __asm__ volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    case 2: __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-    default: __asm__ volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
-    }
-}
-
-/* wait until at most n tiles (8 loads each) are still in flight */
-TL_DEV void wait_tiles(u32 n) {
-    switch (n) {
-    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 2: __asm__ volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-    default: __asm__ volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-    }
-}
-
-/* Ring-kernel tile geometry: a K (or V) tile is 4 KB; a lane owns 16
- * consecutive dims (two 16-byte chunks) of one key in each of the tile's
- * two passes, so LPK = D/16 lanes share a key and every lane holds one key
- * pair (t, t + KPP) for the v_dot2 PV products. */
-template <int D>
-struct RCfg {
-    static constexpr int LPK = D / 16;       /* lanes per key */
-    static constexpr int KPP = 64 / LPK;     /* keys per pass */
-    static constexpr int TK = 2 * KPP;       /* keys per tile */
-    static constexpr int CPR = D / 8;        /* 16-byte chunks per row */
-    static constexpr int UNITS = TK * CPR;   /* 16-byte units per K (or V) tile */
-    static constexpr int LD = UNITS / 64;    /* loads per lane per K (or V) tile */
-};
-
-/* Lazy rescale margin (log2 units): the wave's running max (common to all
- * its lanes) moves only when a score exceeds it by more than this, so
- * probabilities stay <= 2^8 and most tiles skip the rescale. */
-#define TL_DEC_TAU 8.0f
-
-/* Scores, online softmax and PV of one staged tile (keys tbase..tbase+TK-1,
- * those >= kend masked) into the lane group's running state (l, acc); the
- * running max m is common to the wave.  Logical
- * chunk c of tile row t sits at LDS unit t*CPR + (c ^ (t & 1)). */
-template <int D, int G>
-TL_DEV void ring_tile(const uint4 *tk, const uint4 *tv, const u32 (&qr)[G][8], u32 tbase,
-                      u32 kend, int lane, float (&m)[G], float (&l)[G], float (&acc)[G][16]) {
-    using C = RCfg<D>;
-    constexpr int LPK = C::LPK, KPP = C::KPP, CPR = C::CPR;
-    constexpr float NEG_INF = -__builtin_huge_valf();
-    const int g = lane / LPK, sub = lane % LPK;
-    const int t0 = g, t1 = KPP + g;
-    const int c0 = (2 * sub) ^ (g & 1), c1 = (2 * sub + 1) ^ (g & 1);
-    const uint4 ka0 = tk[t0 * CPR + c0], ka1 = tk[t0 * CPR + c1];
-    const uint4 kb0 = tk[t1 * CPR + c0], kb1 = tk[t1 * CPR + c1];
-    const u32 ka[8] = {ka0.x, ka0.y, ka0.z, ka0.w, ka1.x, ka1.y, ka1.z, ka1.w};
-    const u32 kb[8] = {kb0.x, kb0.y, kb0.z, kb0.w, kb1.x, kb1.y, kb1.z, kb1.w};
-    float s0[G], s1[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        float a = 0.f, b = 0.f;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            a = __builtin_amdgcn_fdot2(as_h2(ka[w]), as_h2(qr[h][w]), a, false);
-            b = __builtin_amdgcn_fdot2(as_h2(kb[w]), as_h2(qr[h][w]), b, false);
-        }
-        s0[h] = a;
-        s1[h] = b;
-    }
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        s0[h] = group_sum<LPK>(s0[h]);
-        s1[h] = group_sum<LPK>(s1[h]);
-        /* keep the sums unconditional (the compiler would otherwise move
-         * each dot-product chain into its own divergent branch) */
-        __asm__ volatile("" : "+v"(s0[h]), "+v"(s1[h]));
-    }
-    const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        s0[h] = v0 ? s0[h] : NEG_INF;
-        s1[h] = v1 ? s1[h] : NEG_INF;
-    }
-    const uint4 va0 = tv[t0 * CPR + c0], va1 = tv[t0 * CPR + c1];
-    const uint4 vb0 = tv[t1 * CPR + c0], vb1 = tv[t1 * CPR + c1];
-    u32 pp[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float mx = fmaxf(s0[h], s1[h]);
-        if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
-            /* rare: move the wave's common max to this tile's max */
-            const float mn = group_max<64>(mx);
-            const float alpha = fast_exp2(m[h] - mn);
-            l[h] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
-            m[h] = mn;
-        }
-        const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
-        const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
-        l[h] += p0 + p1;
-        pp[h] = pack_f16x2_fast(p0, p1);
-    }
-    const u32 va[8] = {va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
-    const u32 vb[8] = {vb0.x, vb0.y, vb0.z, vb0.w, vb1.x, vb1.y, vb1.z, vb1.w};
-#pragma unroll
-    for (int w = 0; w < 8; w++) {
-        const half2_t lo = as_h2(perm_lo(va[w], vb[w]));   /* (V[t0][2w], V[t1][2w]) */
-        const half2_t hi = as_h2(perm_hi(va[w], vb[w]));
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            acc[h][2 * w] = __builtin_amdgcn_fdot2(lo, as_h2(pp[h]), acc[h][2 * w], false);
-            acc[h][2 * w + 1] = __builtin_amdgcn_fdot2(hi, as_h2(pp[h]), acc[h][2 * w + 1], false);
-        }
-    }
-}
-
-/* ring_tile over a Q8_0 tile.  The tile's int8 rows are stored as loaded:
- * row t holds D bytes = LPK 16-byte units, and lane (g, sub) reads unit sub
- * of keys t0 = g and t1 = KPP + g (its 16 dims, as in ring_tile: one wave
- * read covers 1 KB of consecutive LDS).  sk / sv hold the tile's binary16
- * scales [TK][D/32]; the lane's 16 dims sit in block sub/2.
- * Scores: the exact int8 values (f16) dot q, times the key's scale (f32).
- * PV: V is dequantized to f16 (q * d rounded once) pairwise across the two
- * keys, then v_dot2 with the packed probabilities as in ring_tile. */
-template <int D, int G>
-TL_DEV void ring_tile_q8(const uint4 *tk, const uint4 *tv, const u16 *sk, const u16 *sv,
-                         const u32 (&qr)[G][8], u32 tbase, u32 kend, int lane, float (&m)[G],
-                         float (&l)[G], float (&acc)[G][16]) {
-    using C = RCfg<D>;
-    constexpr int LPK = C::LPK, KPP = C::KPP, NB = D / 32;
-    constexpr float NEG_INF = -__builtin_huge_valf();
-    const int g = lane / LPK, sub = lane % LPK;
-    const int t0 = g, t1 = KPP + g;
-    const uint4 ka = tk[t0 * LPK + sub], kb = tk[t1 * LPK + sub];
-    const float dk0 = (float)__builtin_bit_cast(_Float16, sk[t0 * NB + sub / 2]);
-    const float dk1 = (float)__builtin_bit_cast(_Float16, sk[t1 * NB + sub / 2]);
-    const u32 kaw[4] = {ka.x, ka.y, ka.z, ka.w}, kbw[4] = {kb.x, kb.y, kb.z, kb.w};
-    half2_t fa[8], fb[8];
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        i8x4_to_f16(kaw[w], fa[2 * w], fa[2 * w + 1]);
-        i8x4_to_f16(kbw[w], fb[2 * w], fb[2 * w + 1]);
-    }
-    float s0[G], s1[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        float a = 0.f, b = 0.f;
-#pragma unroll
-        for (int w = 0; w < 8; w++) {
-            a = __builtin_amdgcn_fdot2(fa[w], as_h2(qr[h][w]), a, false);
-            b = __builtin_amdgcn_fdot2(fb[w], as_h2(qr[h][w]), b, false);
-        }
-        s0[h] = a * dk0;
-        s1[h] = b * dk1;
-    }
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        s0[h] = group_sum<LPK>(s0[h]);
-        s1[h] = group_sum<LPK>(s1[h]);
-        __asm__ volatile("" : "+v"(s0[h]), "+v"(s1[h]));
-    }
-    const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        s0[h] = v0 ? s0[h] : NEG_INF;
-        s1[h] = v1 ? s1[h] : NEG_INF;
-    }
-    const uint4 va = tv[t0 * LPK + sub], vb = tv[t1 * LPK + sub];
-    const u32 dvb = (u32)sv[t0 * NB + sub / 2] | ((u32)sv[t1 * NB + sub / 2] << 16);
-    u32 pp[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float mx = fmaxf(s0[h], s1[h]);
-        if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
-            const float mn = group_max<64>(mx);
-            const float alpha = fast_exp2(m[h] - mn);
-            l[h] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
-            m[h] = mn;
-        }
-        const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
-        const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
-        l[h] += p0 + p1;
-        pp[h] = pack_f16x2_fast(p0, p1);
-    }
-    const half2_t dv2 = as_h2(dvb);                 /* (d of key t0, d of key t1) */
-    const u32 vaw[4] = {va.x, va.y, va.z, va.w}, vbw[4] = {vb.x, vb.y, vb.z, vb.w};
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        /* bytes (a0 b0 a1 b1) and (a2 b2 a3 b3): key pairs of dims 4w .. 4w+3 */
-        const u32 x01 = __builtin_amdgcn_perm(vbw[w], vaw[w], 0x05010400u);
-        const u32 x23 = __builtin_amdgcn_perm(vbw[w], vaw[w], 0x07030602u);
-        half2_t e[4];
-        i8x4_to_f16(x01, e[0], e[1]);
-        i8x4_to_f16(x23, e[2], e[3]);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const half2_t vv = e[k] * dv2;
-#pragma unroll
-            for (int h = 0; h < G; h++)
-                acc[h][4 * w + k] = __builtin_amdgcn_fdot2(vv, as_h2(pp[h]), acc[h][4 * w + k], false);
-        }
-    }
-}
-
-constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 : x >= 2 ? 2 : 1; }
-
-/* Merge of a group's n_split partials by its last workgroup, in registers:
- * TPC threads per output float4 (h, d..d+3) each fold their share of the
- * splits with an online max, then combine across the TPC lanes with DPP:
- * out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s.  The first
- * batch of partial rows and every (m, l) pair are requested together
- * (device-coherent loads); the pairs go through LDS (s_ml: G*n_split). */
-template <int D, int G, int NT>
-TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const DecSeq &sq,
-                             float2 *s_ml) {
-    constexpr float NEG_INF = -__builtin_huge_valf();
-    constexpr int COLS = G * D / 4;
-    constexpr int TPC = pow2_floor(NT / COLS > 16 ? 16 : (NT / COLS < 1 ? 1 : NT / COLS));
-    constexpr int K = 8;                       /* splits per load batch */
-    const int tid = threadIdx.x;
-    const u32 ns = p.n_split;
-    const __amdgpu_buffer_rsrc_t rml = buf_rsrc(p.ws_ml + pb);
-    const __amdgpu_buffer_rsrc_t racc = buf_rsrc(p.ws_acc + (u64)pb * D);
-    const int part = tid % TPC;
-    const int col0 = tid / TPC;
-    u32x4v_t a[K];
-    auto load_batch = [&](int col, u32 s0) {
-        const int h = col / (D / 4), d = (col % (D / 4)) * 4;
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-            const u32 s = min(s0 + k * TPC, ns - 1);
-            const u32 off = (((u32)h * ns + s) * D + d) * 4;
-            a[k] = __builtin_amdgcn_raw_buffer_load_b128(racc, off, 0, TL_SC1);
-        }
-    };
-    if (col0 < COLS) load_batch(col0, (u32)part);
-    for (u32 i = tid; i < (u32)G * ns; i += NT) {
-        const u32x2v_t ml = __builtin_amdgcn_raw_buffer_load_b64(rml, i * 8, 0, TL_SC1);
-        s_ml[i] = make_float2(__uint_as_float(ml[0]), __uint_as_float(ml[1]));
-    }
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    TL_TRACE(10);
-    for (int col = col0; col < COLS; col += NT / TPC) {
-        const int h = col / (D / 4), d = (col % (D / 4)) * 4;
-        const float2 *mlh = s_ml + (u32)h * ns;
-        float M = NEG_INF, L = 0.f;
-        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (u32 s0 = part; s0 < ns; s0 += K * TPC) {
-            if (col != col0 || s0 != (u32)part) load_batch(col, s0);
-            float2 ml[K];
-            float bm = NEG_INF;
-#pragma unroll
-            for (int k = 0; k < K; k++) {
-                const u32 s = s0 + k * TPC;
-                ml[k] = mlh[min(s, ns - 1)];
-                if (s >= ns) ml[k] = make_float2(NEG_INF, 0.f);   /* past the last split */
-                bm = fmaxf(bm, ml[k].x);
-            }
-            const float nm = fmaxf(M, bm);
-            const float mu = (nm == NEG_INF) ? 0.f : nm;
-            const float sc = fast_exp2(M - mu);
-            L *= sc;
-            O.x *= sc; O.y *= sc; O.z *= sc; O.w *= sc;
-            M = nm;
-#pragma unroll
-            for (int k = 0; k < K; k++) {
-                const float w = fast_exp2(ml[k].x - mu);
-                L = fmaf(w, ml[k].y, L);
-                O.x = fmaf(w, __uint_as_float(a[k][0]), O.x);
-                O.y = fmaf(w, __uint_as_float(a[k][1]), O.y);
-                O.z = fmaf(w, __uint_as_float(a[k][2]), O.z);
-                O.w = fmaf(w, __uint_as_float(a[k][3]), O.w);
-            }
-        }
-        if constexpr (TPC > 1) {
-            const float Mg = group_max<TPC>(M);
-            const float mu = (Mg == NEG_INF) ? 0.f : Mg;
-            const float e = fast_exp2(M - mu);
-            L = group_sum<TPC>(L * e);
-            O.x = group_sum<TPC>(O.x * e);
-            O.y = group_sum<TPC>(O.y * e);
-            O.z = group_sum<TPC>(O.z * e);
-            O.w = group_sum<TPC>(O.w * e);
-        }
-        if (part == 0) {
-            const float inv = 1.0f / L;
-            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)(kvh * G + h) * D + d] =
-                make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
-        }
-    }
-}
-
-/* Decode attention with one workgroup of 8 waves per CU.  Each wave streams
- * its tiles (every 8th tile of the chunk) through a ring of two LDS stages
- * filled by LDS-direct loads: while one tile is computed the next is in
- * flight, and two waves per SIMD hide each other's latency.  Every group of
- * LPK lanes keeps its own online-softmax state (no cross-lane exchange in
- * the stream loop); the groups and waves merge once at the end.  Split
- * decomposition, XCD-aware block order, GQA sharing, the fused append and
- * the split merge are described at the top of this file.  Tiles that hold rows
- * appended by this launch (the last tiles of the last split) are filled
- * from registers after the ring has drained. */
-#define TL_RING_WAVES 8
-#ifndef TL_XCD_ROT
-#define TL_XCD_ROT 0
-#endif
-#define TL_RING_STAGES 2
-template <int D, int G, bool ROPE, bool Q8>
-__global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
-    using C = RCfg<D>;
-    constexpr int LPK = C::LPK, CPR = C::CPR, TK = C::TK, UNITS = C::UNITS, LD = C::LD;
-    /* a Q8_0 tile is half the bytes of an f16 one: twice the stages in the
-     * same ring memory, plus the scales (64 words per stage) */
-    constexpr int W = TL_RING_WAVES, S = Q8 ? 2 * TL_RING_STAGES : TL_RING_STAGES, NT = 64 * W;
-    constexpr int STAGE_U = Q8 ? UNITS : 2 * UNITS;   /* 16-byte units per stage (K + V) */
-    constexpr int RING_U = 2 * TL_RING_STAGES * UNITS;
-    constexpr int VPR = D / 8;
-    constexpr float NEG_INF = -__builtin_huge_valf();
-    static_assert(LD == 4, "wait_tiles assumes 8 loads per tile");
-    static_assert(S * STAGE_U <= RING_U, "ring stages");
-
-    __shared__ uint4 s_ring[W][RING_U];          /* per wave: S stages of (K, V) */
-    __shared__ u32 s_scl[Q8 ? W : 1][Q8 ? S * 64 : 1];
-    __shared__ u32 s_slot[TL_DEC_MAX_CHUNK];
-    __shared__ uint4 s_q[G * D / 8];
-    __shared__ float s_m[W][G];
-    __shared__ uint4 s_newk[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
-    __shared__ uint4 s_newv[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    TL_TRACE(0);
-    TL_TRACE_IDS();
-
-    const u32 n_split = p.n_split;
-    const u32 n_groups = gridDim.x / n_split;
-    const u32 bid = blockIdx.x;
-    u32 grp, split;
-    if ((n_groups & 7) == 0) {
-        const u32 xcd = bid & 7, local = bid >> 3;
-        grp = ((xcd + TL_XCD_ROT) & 7) + 8 * (local / n_split);
-        split = local % n_split;
-    } else {
-        grp = bid / n_split;
-        split = bid % n_split;
-    }
-    const u32 kvh = grp % p.n_kv;
-    const u32 grow = grp / p.n_kv;
-    const u32 si = grow / p.rows_per_seq;
-    const u32 r = grow % p.rows_per_seq;
-    const DecSeq sq = p.seq[si];
-
-    const u32 n_keys = sq.pos + r + 1;
-    const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
-    const u32 kbeg = start + split * p.chunk;
-    const u32 kend = min(kbeg + p.chunk, n_keys);
-    const bool fused = !Q8 && sq.kin != nullptr;
-    const bool writer = fused && split == 0 && r == 0;
-    const bool need_new = fused && (writer || kend > sq.pos);
-    const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
-
-    /* physical rows of the chunk's keys */
-    const bool staged = (sq.ring == 0) && (sq.slots != nullptr);
-    if (staged)
-        for (u32 i = kbeg + tid; i < kend; i += NT) {
-            const u32 s = sq.slots[i];
-            s_slot[i - kbeg] = s < sq.cap ? s : 0u;
-        }
-    /* q of the GQA group (RoPE'd at pos + r when ROPE), scaled to log2 units,
-     * f16; the launch's new K/V rows (K RoPE'd at pos + row), f16 */
-    const float sc = p.scale_log2;
-    if constexpr (ROPE) {
-        const u32 pairs = p.rope.rdim >> 1;
-        u16 *q16 = (u16 *)s_q;
-        for (u32 t = tid; t < (u32)G * (D / 2); t += NT) {
-            const u32 h = t / (D / 2), i = t % (D / 2);
-            const float *row = qb + h * D;
-            u32 ia, ib;
-            float x, y;
-            if (i < pairs) {
-                ia = p.rope.neox ? i : 2 * i;
-                ib = p.rope.neox ? i + pairs : 2 * i + 1;
-                float c, sn;
-                rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
-                rope_rot(row[ia], row[ib], c, sn, x, y);
-            } else {
-                ia = 2 * i;
-                ib = 2 * i + 1;
-                x = row[ia];
-                y = row[ib];
-            }
-            const u32 pk = pack_f16x2_fast(x * sc, y * sc);
-            q16[h * D + ia] = (u16)(pk & 0xffffu);
-            q16[h * D + ib] = (u16)(pk >> 16);
-        }
-        if (need_new) {
-            for (u32 t = tid; t < p.rows_per_seq * (D / 2); t += NT) {
-                const u32 row = t / (D / 2), i = t % (D / 2);
-                const float *src = sq.kin + (u64)row * sq.kv_stride + (u64)kvh * D;
-                u32 ia, ib;
-                float x, y;
-                if (i < pairs) {
-                    ia = p.rope.neox ? i : 2 * i;
-                    ib = p.rope.neox ? i + pairs : 2 * i + 1;
-                    float c, sn;
-                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + row, c, sn);
-                    rope_rot(src[ia], src[ib], c, sn, x, y);
-                } else {
-                    ia = 2 * i;
-                    ib = 2 * i + 1;
-                    x = src[ia];
-                    y = src[ib];
-                }
-                u16 *k16 = (u16 *)s_newk[row];
-                k16[ia] = (u16)f32_to_f16_bits(x);
-                k16[ib] = (u16)f32_to_f16_bits(y);
-            }
-            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
-                const u32 row = i / VPR, c8 = i % VPR;
-                s_newv[row][c8] = cvt8_f16(sq.vin + (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8);
-            }
-        }
-    } else {
-        for (int i = tid; i < G * D / 8; i += NT) {
-            const float4 a = *(const float4 *)(qb + i * 8);
-            const float4 b = *(const float4 *)(qb + i * 8 + 4);
-            s_q[i] = make_uint4(pack_f16x2_fast(a.x * sc, a.y * sc), pack_f16x2_fast(a.z * sc, a.w * sc),
-                                pack_f16x2_fast(b.x * sc, b.y * sc), pack_f16x2_fast(b.z * sc, b.w * sc));
-        }
-        if (need_new)
-            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
-                const u32 row = i / VPR, c8 = i % VPR;
-                const u64 src = (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8;
-                s_newk[row][c8] = cvt8_f16(sq.kin + src);
-                s_newv[row][c8] = cvt8_f16(sq.vin + src);
-            }
-    }
-    __syncthreads();
-    TL_TRACE(1);
-
-    const u16 *Kbase = sq.k + (u64)kvh * sq.cap * D;
-    const u16 *Vbase = sq.v + (u64)kvh * sq.cap * D;
-    const u32 ring_lds = (u32)(uintptr_t)&s_ring[wave][0];
-    /* Q8_0: int8 rows and their scale planes (f16 [n_kv][cap][D/32]) */
-    const uint8_t *K8 = (const uint8_t *)sq.k + (u64)kvh * sq.cap * D;
-    const uint8_t *V8 = (const uint8_t *)sq.v + (u64)kvh * sq.cap * D;
-    const u16 *KS = Q8 ? sq.ks + (u64)kvh * sq.cap * (D / 32) : nullptr;
-    const u16 *VS = Q8 ? sq.vs + (u64)kvh * sq.cap * (D / 32) : nullptr;
-    const u32 scl_lds = (u32)(uintptr_t)&s_scl[Q8 ? wave : 0][0];
-
-    /* tiles of the chunk: the first n_dma (entirely cache rows written
-     * before this launch) stream through the ring; the rest hold new rows */
-    const u32 ntile = (kend > kbeg) ? (kend - kbeg + TK - 1) / TK : 0;
-    u32 n_dma = ntile;
-    if (fused && kend > sq.pos) n_dma = sq.pos > kbeg ? (sq.pos - kbeg) / TK : 0;
-    const u32 nj = n_dma > (u32)wave ? (n_dma - wave + W - 1) / W : 0;   /* this wave's ring tiles */
-    const u32 klast = kend - 1;
-
-    auto phys = [&](u32 key) -> u32 {
-        if (sq.ring) return key % sq.ring;
-        return staged ? s_slot[key - kbeg] : key;
-    };
-    /* unit u = jj*64 + lane of a K (or V) tile holds chunk (u % CPR) ^ (row & 1)
-     * of tile row u / CPR.  Rows past the chunk load its last row (their
-     * scores are masked to -inf, so they add exactly 0). */
-    auto issue = [&](u32 j) {
-        const u32 tb = kbeg + (wave + W * j) * TK;
-        const u32 lk = ring_lds + (j % S) * (STAGE_U * 16);
-        if constexpr (Q8) {
-            /* values: unit u = jj*64 + lane is 16-byte unit u % LPK of tile
-             * row u / LPK, stored as loaded; K then V (UNITS/2 units each) */
-#pragma unroll
-            for (int jj = 0; jj < LD / 2; jj++) {
-                const int u = jj * 64 + lane;
-                const u32 ph = phys(min(tb + (u32)(u / LPK), klast));
-                const u32 off = ph * D + (u % LPK) * 16;
-                lds_dma16(lk + jj * 1024, K8, off);
-                lds_dma16(lk + UNITS * 8 + jj * 1024, V8, off);
-            }
-            /* scales: 32 words per plane (TK rows x D/32 f16), lanes 0..31 */
-            const int srow = lane / (D / 64), sw = lane % (D / 64);
-            const u32 sph = phys(min(tb + (u32)srow, klast));
-            const u32 soff = (sph * (D / 32) + 2 * sw) * 2;
-            const u32 ls = scl_lds + (j % S) * 256;
-#ifndef TL_Q8_NOSCALE
-            if (lane < 32) {
-                lds_dma4(ls, KS, soff);
-                lds_dma4(ls + 128, VS, soff);
-            }
-#endif
-            return;
-        }
-#pragma unroll
-        for (int jj = 0; jj < LD; jj++) {
-            const int u = jj * 64 + lane;
-            const int row = u / CPR;
-            const u32 ph = phys(min(tb + (u32)row, klast));
-            const u32 off = (ph * D + (((u % CPR) ^ (row & 1)) * 8)) * 2;
-            lds_dma16(lk + jj * 1024, Kbase, off);
-            lds_dma16(lk + UNITS * 16 + jj * 1024, Vbase, off);
-        }
-    };
-
-    const u32 npre = nj < (u32)S ? nj : (u32)S;
-    for (u32 j = 0; j < npre; j++) issue(j);
-
-    /* q of this lane's 16 dims, every head of the group */
-    u32 qr[G][8];
-    {
-        const int sub = lane % LPK;
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            const uint4 a = s_q[h * CPR + 2 * sub], b = s_q[h * CPR + 2 * sub + 1];
-            qr[h][0] = a.x; qr[h][1] = a.y; qr[h][2] = a.z; qr[h][3] = a.w;
-            qr[h][4] = b.x; qr[h][5] = b.y; qr[h][6] = b.z; qr[h][7] = b.w;
-        }
-    }
-    float m[G], l[G], acc[G][16];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        m[h] = NEG_INF;
-        l[h] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[h][e] = 0.f;
-    }
-
-    for (u32 j = 0; j < nj; j++) {
-        const u32 after = nj - 1 - j;
-        if constexpr (Q8)
-            wait_tiles_q8(after < (u32)(S - 1) ? after : (u32)(S - 1));
-        else
-            wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
-#ifdef TL_DEC_TRACE
-        if (j == 0 && lane == 0 && blockIdx.x < 8192)
-            tl_dec_trace[blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();
-#endif
-#ifndef TL_DEC_NOCOMPUTE
-        const uint4 *st = &s_ring[wave][(j % S) * STAGE_U];
-        if constexpr (Q8) {
-            const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
-            ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
-                               kend, lane, m, l, acc);
-        } else {
-            ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
-        }
-#endif
-        if (j + S < nj) issue(j + S);
-    }
-    /* tiles with new rows: cache rows and staged new rows through registers */
-    if constexpr (!Q8)
-    for (u32 t = n_dma + ((u32)wave + W - n_dma % W) % W; t < ntile; t += W) {
-        uint4 *tk = &s_ring[wave][0];
-        uint4 *tv = &s_ring[wave][UNITS];
-        const u32 tb = kbeg + t * TK;
-#pragma unroll
-        for (int jj = 0; jj < LD; jj++) {
-            const int u = jj * 64 + lane;
-            const int row = u / CPR;
-            const u32 key = min(tb + (u32)row, klast);
-            const int c = (u % CPR) ^ (row & 1);
-            uint4 a, b;
-            if (key >= sq.pos) {
-                a = s_newk[key - sq.pos][c];
-                b = s_newv[key - sq.pos][c];
-            } else {
-                const u32 ph = phys(key);
-                a = ld_stream(Kbase + (u64)ph * D + c * 8);
-                b = ld_stream(Vbase + (u64)ph * D + c * 8);
-            }
-            tk[u] = a;
-            tv[u] = b;
-        }
-        __builtin_amdgcn_wave_barrier();
-        ring_tile<D, G>(tk, tv, qr, tb, kend, lane, m, l, acc);
-        __builtin_amdgcn_wave_barrier();
-    }
-    if (!Q8 && writer) {
-        for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
-            const u32 row = i / VPR, c8 = i % VPR;
-            const u32 key = sq.pos + row;
-            const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
-            if (ph >= sq.cap) continue;
-            const u64 dst = ((u64)kvh * sq.cap + ph) * D + c8 * 8;
-            *(uint4 *)((u16 *)sq.k + dst) = s_newk[row][c8];
-            *(uint4 *)((u16 *)sq.v + dst) = s_newv[row][c8];
-        }
-    }
-
-    /* ---- one state per workgroup and head ----
-     * The running max is wave-uniform, so the lanes of a wave add directly;
-     * the waves combine with weights exp2(m_w - M_h).  A wave that has
-     * finished its tiles writes its state into its own ring region (no
-     * barrier: that region is no longer read): acc as float4
-     * [head][k4][lane] (up to HB heads, 16 KB), l per lane group.  After
-     * one barrier, TPC threads per output float4 each add a share of the
-     * W * GPW lane groups (lanes sub + LPK*part: every 8-lane phase of a
-     * read touches distinct banks), then add across with shuffles.  More
-     * than HB heads take further rounds through the same memory. */
-    constexpr int GPW = 64 / LPK;                     /* lane groups per wave */
-    constexpr int NGRP = W * GPW;                     /* lane groups per workgroup */
-    constexpr int HB = G < 4 ? G : 4;                 /* heads per round */
-    constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
-    constexpr int TPC0 = NT / COLB > GPW ? GPW : NT / COLB;
-    constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
-    constexpr int WREG = RING_U;                      /* float4 per wave region */
-    static_assert(HB * 4 * 64 <= WREG, "wave state exceeds its ring region");
-    static_assert(GPW % TPC == 0, "lane groups per thread");
-    __shared__ float s_lg[G][NGRP];
-    float4 *s_w4 = (float4 *)&s_ring[0][0];
-    const int sub = lane % LPK, gi = lane / LPK;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        if (sub == 0) s_lg[h][wave * GPW + gi] = l[h];
-        if (lane == 0) s_m[wave][h] = m[h];
-    }
-    const bool single = (n_split == 1);
-    const bool last_merges = p.counters != nullptr;
-    const u32 pb = (grow * p.n_head + kvh * G) * n_split;
-    /* reader mapping: t -> (sub, part, k4, hh) */
-    const int rsub = tid % LPK, rpart = (tid / LPK) % TPC, rest = tid / (LPK * TPC);
-    const int rk4 = rest % 4, rhh = rest / 4;
-#pragma unroll
-    for (int h0 = 0; h0 < G; h0 += HB) {
-        if (h0) __syncthreads();                      /* previous round read */
-        float4 *mine = s_w4 + wave * WREG;
-#pragma unroll
-        for (int hh = 0; hh < HB; hh++)
-            if (h0 + hh < G)
-#pragma unroll
-                for (int k4 = 0; k4 < 4; k4++)
-                    mine[(hh * 4 + k4) * 64 + lane] =
-                        make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
-                                    acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
-        __syncthreads();
-        if (h0 == 0) TL_TRACE(2);
-        if (h0 == 0) TL_TRACE(8);
-        const int h = h0 + rhh;
-        if (rhh < HB && h < G) {
-            const int d = rsub * 16 + rk4 * 4;
-            float mm = s_m[0][h];
-#pragma unroll
-            for (int w = 1; w < W; w++) mm = fmaxf(mm, s_m[w][h]);
-            const float mu = (mm == NEG_INF) ? 0.f : mm;
-            float L = 0.f;
-            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 *src = s_w4 + (rhh * 4 + rk4) * 64 + rsub;
-#pragma unroll
-            for (int w = 0; w < W; w++) {
-                const float e = fast_exp2(s_m[w][h] - mu);
-                float lw = 0.f;
-                float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int g = 0; g < GPW; g += TPC) {
-                    const float4 t = src[w * WREG + (g + rpart) * LPK];
-                    lw += s_lg[h][w * GPW + g + rpart];
-                    a.x += t.x; a.y += t.y; a.z += t.z; a.w += t.w;
-                }
-                L = fmaf(e, lw, L);
-                O.x = fmaf(e, a.x, O.x);
-                O.y = fmaf(e, a.y, O.y);
-                O.z = fmaf(e, a.z, O.z);
-                O.w = fmaf(e, a.w, O.w);
-            }
-#pragma unroll
-            for (int x = LPK; x < LPK * TPC; x *= 2) {
-                L += __shfl_xor(L, x);
-                O.x += __shfl_xor(O.x, x);
-                O.y += __shfl_xor(O.y, x);
-                O.z += __shfl_xor(O.z, x);
-                O.w += __shfl_xor(O.w, x);
-            }
-            if (rpart == 0) {
-                const u32 hq = kvh * G + h;
-                if (single) {
-                    const float inv = 1.0f / L;
-                    *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] =
-                        make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
-                } else if (last_merges) {
-                    /* device-coherent stores: the merging workgroup may run
-                     * on another XCD and reads them with device-coherent loads */
-                    const u32 pi = (u32)h * n_split + split;
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        u32x4v_t{__float_as_uint(O.x), __float_as_uint(O.y), __float_as_uint(O.z),
-                                 __float_as_uint(O.w)},
-                        buf_rsrc(p.ws_acc + (u64)pb * D), (pi * D + d) * 4, 0, TL_SC1);
-                    if (d == 0)
-                        __builtin_amdgcn_raw_buffer_store_b64(
-                            u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
-                            buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
-                } else {
-                    const u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
-                    *(float4 *)&p.ws_acc[pi * D + d] = O;
-                    if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
-                }
-            }
-        }
-    }
-    if (single || !last_merges) return;
-
-    /* ---- the last split of this (row, kv-head) group to finish merges ----
-     * Its partial stores are complete (vmcnt 0) before the counter add, so
-     * the workgroup that sees n_split - 1 reads every partial. */
-    __shared__ u32 s_last;
-    TL_TRACE(12);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    TL_TRACE(3);
-    if (tid == 0)
-        s_last = __hip_atomic_fetch_add(&p.counters[grp], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_last != n_split - 1) return;
-    if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    TL_TRACE(9);
-    /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */
-    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0]);
-#ifdef TL_DEC_TRACE
-    __syncthreads();
-    TL_TRACE(4);
-#endif
-}
-
-/* One decode kernel instance: entry point, K (or V) bytes per wave tile and
- * threads per workgroup.  The RoPE-fusing instances are separate so the
- * plain ones carry none of its code. */
-struct DecKernel {
-    const void *fn;
-    int tile_bytes;
-    int threads;
-};
+#include "tl_decode_kernels.h"
 
 template <int D>
 static DecKernel pick_kernel(int G, bool rope, bool q8) {
+    if (q8) return tl_pick_decode_q8(D, G, rope);   /* tl_decode_q8.hip */
     constexpr int NT = 64 * TL_RING_WAVES;
     switch (G) {
 #define TL_CASE(g)                                                                          \
     case g:                                                                                 \
-        if (q8) return {(const void *)attn_decode_ring_kernel<D, g, false, true>, 4096, NT}; \
         if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true, false>, 4096, NT}; \
         return {(const void *)attn_decode_ring_kernel<D, g, false, false>, 4096, NT};
         TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
@@ -1000,7 +97,6 @@ static int resident_per_cu(const void *fn, int threads) {
 int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
                      u32 max_vis, hipStream_t st, bool q8) {
     if (q8) {
-        if (p.rope.rdim) return tl_fail(TL_EINVAL, "decode: no fused RoPE over a Q8_0 cache");
         for (u32 i = 0; i < TL_MAX_BATCH_SEQ; i++)
             if (p.seq[i].kin) return tl_fail(TL_EINVAL, "decode: no fused append into a Q8_0 cache");
     }

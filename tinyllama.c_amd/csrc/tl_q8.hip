@@ -13,9 +13,10 @@
  * (src/backend/gpu/gpu.cu:1077-1086): amax = max |x|, d = amax / 127,
  * id = d > 0 ? 1/d : 0, q = rint(x * id); d is stored RNE as binary16.
  *
- *   kv_append_q8_kernel  8 lanes per 32-element block: one float4 of K and
- *                        of V each, the block max by DPP within the 8 lanes,
- *                        one 4-byte store of q per lane, lane 0 the scale.
+ *   kv_append_q8_kernel  4 lanes per 32-element block: 8 values of K (RoPE'd
+ *                        on the way when asked) and of V each, the block max
+ *                        by DPP within the 4 lanes, one 8-byte store of q per
+ *                        lane, lane 0 the scale.
  *   kv_gather_q8_kernel  rows by slot (values and scales).
  *   kv_copy_q8_kernel    row copies across layers (fork / compaction).
  * Attention: decode-sized batches run the split-K ring kernel's Q8_0
@@ -117,38 +118,64 @@ struct Q8AppendSeg {
 };
 struct Q8AppendParams {
     Q8AppendSeg seg[TL_MAX_BATCH_SEQ];
+    RopeCfg rope;            /* applied to K before quantizing (rdim 0: none) */
 };
 
-/* 4 values of a block whose scale is 1/id -> 4 int8 in one word */
-TL_DEV u32 q8_pack4(float4 x, float id) {
-    const int a = (int)rintf(x.x * id), b = (int)rintf(x.y * id);
-    const int c = (int)rintf(x.z * id), d = (int)rintf(x.w * id);
-    return (u32)(a & 0xff) | ((u32)(b & 0xff) << 8) | ((u32)(c & 0xff) << 16) |
-           ((u32)(d & 0xff) << 24);
+/* 8 values of a block whose scale is 1/id -> 8 int8 in two words */
+TL_DEV uint2 q8_pack8(const float (&x)[8], float id) {
+    u32 w[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int a = (int)rintf(x[4 * h] * id), b = (int)rintf(x[4 * h + 1] * id);
+        const int c = (int)rintf(x[4 * h + 2] * id), d = (int)rintf(x[4 * h + 3] * id);
+        w[h] = (u32)(a & 0xff) | ((u32)(b & 0xff) << 8) | ((u32)(c & 0xff) << 16) |
+               ((u32)(d & 0xff) << 24);
+    }
+    return make_uint2(w[0], w[1]);
 }
 
-TL_DEV float amax4(float4 x) {
-    return fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+TL_DEV float amax8(const float (&x)[8]) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(x[j]));
+    return m;
 }
 
-/* grid: (blocks, segments).  One lane per 4 elements; the 8 lanes of a block
- * are an aligned group of a wave (grid stride and row length are multiples
- * of 8), so the block max is a DPP max within the group. */
+/* grid: (blocks, segments).  One lane per 8 elements (K RoPE'd first when
+ * ROPE, by the routine rope_kernel uses, so the bits equal tl_rope then the
+ * plain append); the 4 lanes of a block are an aligned group of a wave
+ * (grid stride and row length are multiples of 4), so the block max is a
+ * DPP max within the group. */
+template <bool ROPE>
 __global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams pp) {
     const Q8AppendSeg &p = pp.seg[blockIdx.y];
-    const u32 qpr = p.head_dim >> 2;
-    const u64 total = (u64)p.n * p.n_kv * qpr;
+    const u32 opr = p.head_dim >> 3;
+    const u64 total = (u64)p.n * p.n_kv * opr;
     for (u64 idx = (u64)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (u64)gridDim.x * blockDim.x) {
-        const u32 e = (u32)(idx % qpr);
-        const u64 t = idx / qpr;
+        const u32 e = (u32)(idx % opr);
+        const u64 t = idx / opr;
         const u32 h = (u32)(t % p.n_kv);
         const u32 i = (u32)(t / p.n_kv);
-        const u64 src = (u64)i * p.kv_stride + (u64)h * p.head_dim + e * 4;
-        const float4 kx = *(const float4 *)(p.k + src);
-        const float4 vx = *(const float4 *)(p.v + src);
-        const float kmax = group_max<8>(amax4(kx));
-        const float vmax = group_max<8>(amax4(vx));
+        const u64 rowoff = (u64)i * p.kv_stride + (u64)h * p.head_dim;
+        float kx[8], vx[8];
+        if constexpr (ROPE) {
+            load8_rope(p.k + rowoff, e * 8, p.pos + i, pp.rope.rdim, pp.rope.theta,
+                       pp.rope.neox, kx);
+        } else {
+            const float4 a = *(const float4 *)(p.k + rowoff + e * 8);
+            const float4 b = *(const float4 *)(p.k + rowoff + e * 8 + 4);
+            kx[0] = a.x; kx[1] = a.y; kx[2] = a.z; kx[3] = a.w;
+            kx[4] = b.x; kx[5] = b.y; kx[6] = b.z; kx[7] = b.w;
+        }
+        {
+            const float4 a = *(const float4 *)(p.v + rowoff + e * 8);
+            const float4 b = *(const float4 *)(p.v + rowoff + e * 8 + 4);
+            vx[0] = a.x; vx[1] = a.y; vx[2] = a.z; vx[3] = a.w;
+            vx[4] = b.x; vx[5] = b.y; vx[6] = b.z; vx[7] = b.w;
+        }
+        const float kmax = group_max<4>(amax8(kx));
+        const float vmax = group_max<4>(amax8(vx));
         const u32 key = p.pos + i;
         const u32 slot = p.ring ? key % p.ring : (p.slots ? p.slots[key] : key);
         if (slot >= p.cap) continue;
@@ -156,11 +183,11 @@ __global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams 
         const float ik = dk > 0.0f ? 1.0f / dk : 0.0f;
         const float iv = dv > 0.0f ? 1.0f / dv : 0.0f;
         const u64 row = (u64)h * p.cap + slot;
-        *(u32 *)(p.k8 + row * p.head_dim + e * 4) = q8_pack4(kx, ik);
-        *(u32 *)(p.v8 + row * p.head_dim + e * 4) = q8_pack4(vx, iv);
-        if ((e & 7) == 0) {
-            p.ks[row * (p.head_dim / 32) + e / 8] = (u16)f32_to_f16_bits(dk);
-            p.vs[row * (p.head_dim / 32) + e / 8] = (u16)f32_to_f16_bits(dv);
+        *(uint2 *)(p.k8 + row * p.head_dim + e * 8) = q8_pack8(kx, ik);
+        *(uint2 *)(p.v8 + row * p.head_dim + e * 8) = q8_pack8(vx, iv);
+        if ((e & 3) == 0) {
+            p.ks[row * (p.head_dim / 32) + e / 4] = (u16)f32_to_f16_bits(dk);
+            p.vs[row * (p.head_dim / 32) + e / 4] = (u16)f32_to_f16_bits(dv);
         }
     }
 }
@@ -191,24 +218,28 @@ static int fill_seg_q8(Q8AppendSeg &p, const tl_kv_layer_q8 *L, const float *k, 
 static int launch_append_q8(const Q8AppendParams &p, u32 n_seg, hipStream_t st) {
     u64 most = 0;
     for (u32 i = 0; i < n_seg; i++) {
-        const u64 t = (u64)p.seg[i].n * p.seg[i].n_kv * (p.seg[i].head_dim / 4);
+        const u64 t = (u64)p.seg[i].n * p.seg[i].n_kv * (p.seg[i].head_dim / 8);
         if (t > most) most = t;
     }
     if (most == 0) return TL_OK;
     u64 blocks = (most + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(kv_append_q8_kernel, dim3((u32)blocks, n_seg), dim3(256), 0, st, p);
+    if (p.rope.rdim)
+        hipLaunchKernelGGL(kv_append_q8_kernel<true>, dim3((u32)blocks, n_seg), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(kv_append_q8_kernel<false>, dim3((u32)blocks, n_seg), dim3(256), 0, st, p);
     HIP_TRY(hipGetLastError());
     return TL_OK;
 }
 
 static int append_q8(const tl_kv_layer_q8 *L, const float *k, const float *v, u32 kv_stride,
-                     const u32 *slots, u32 pos, u32 n, hipStream_t st) {
+                     const u32 *slots, u32 pos, u32 n, const RopeCfg &rope, hipStream_t st) {
     if (n == 0) return TL_OK;
     Q8AppendParams p;
     memset(&p, 0, sizeof(p));
     int rc = fill_seg_q8(p.seg[0], L, k, v, kv_stride, slots, pos, n);
     if (rc) return rc;
+    p.rope = rope;
     return launch_append_q8(p, 1, st);
 }
 
@@ -217,7 +248,20 @@ extern "C" int tl_kv_append_q8(const tl_kv_layer_q8 *L, const float *k, const fl
                                uint32_t n, void *stream) {
     int rc = check_layer_q8(L);
     if (rc) return rc;
-    return append_q8(L, k, v, kv_stride, slots, pos, n, (hipStream_t)stream);
+    RopeCfg none;
+    tl_rope_cfg(L->head_dim, nullptr, none);
+    return append_q8(L, k, v, kv_stride, slots, pos, n, none, (hipStream_t)stream);
+}
+
+extern "C" int tl_kv_append_rope_q8(const tl_kv_layer_q8 *L, const float *k, const float *v,
+                                    uint32_t kv_stride, const uint32_t *slots, uint32_t pos,
+                                    uint32_t n, const tl_rope_params *rope, void *stream) {
+    int rc = check_layer_q8(L);
+    if (rc) return rc;
+    RopeCfg c;
+    rc = tl_rope_cfg(L->head_dim, rope, c);
+    if (rc) return rc;
+    return append_q8(L, k, v, kv_stride, slots, pos, n, c, (hipStream_t)stream);
 }
 
 extern "C" int tl_kv_append_layers_q8(const tl_kv_layer_q8 *layers, uint32_t n_layer,
@@ -400,21 +444,22 @@ extern "C" int tl_kv_copy_between_q8(const tl_kv_layer_q8 *dst_layers,
 /* ------------------------------------------------------------------------ */
 
 static int attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, bool append,
-                   hipStream_t st) {
+                   const tl_rope_params *rp, hipStream_t st) {
     int rc = check_layer_q8(L);
     if (rc) return rc;
     const LayerView lv = view_q8(L);
     rc = tl_check_attn_args(lv, a);
     if (rc) return rc;
+    RopeCfg rope;
+    rc = tl_rope_cfg(L->head_dim, rp, rope);
+    if (rc) return rc;
     if (a->n == 0) return TL_OK;
     if (append) {
-        rc = append_q8(L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n, st);
+        rc = append_q8(L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n, rope, st);
         if (rc) return rc;
     }
-    RopeCfg none;
-    tl_rope_cfg(L->head_dim, nullptr, none);
     if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(lv, a))
-        return tl_launch_prefill(lv, a, none, st);
+        return tl_launch_prefill(lv, a, rope, st);
     DecParams p;
     memset(&p, 0, sizeof(p));
     p.seq[0].k = (const u16 *)L->k;
@@ -433,19 +478,24 @@ static int attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, bool append,
     p.q_stride = a->q_stride;
     p.window = a->window;
     p.scale_log2 = a->scale * 1.4426950408889634f;
-    p.rope = none;
+    p.rope = rope;
     const u32 max_keys = a->pos + a->n;
     const u32 max_vis = (a->window && max_keys > a->window) ? a->window : max_keys;
     return tl_launch_decode(p, a->n, L->head_dim, a->n_head / L->n_kv_head, max_vis, st, true);
 }
 
 extern "C" int tl_attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, void *stream) {
-    return attn_q8(L, a, true, (hipStream_t)stream);
+    return attn_q8(L, a, true, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int tl_attn_rope_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a,
+                               const tl_rope_params *rope, void *stream) {
+    return attn_q8(L, a, true, rope, (hipStream_t)stream);
 }
 
 extern "C" int tl_attn_noappend_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a,
                                    void *stream) {
-    return attn_q8(L, a, false, (hipStream_t)stream);
+    return attn_q8(L, a, false, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int tl_attn_decode_batch_q8(const tl_decode_seq_q8 *seqs, uint32_t n_seq,

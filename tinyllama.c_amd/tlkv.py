@@ -102,6 +102,10 @@ def lib():
                                   vp, u32, vp],
         "tl_attn_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_noappend_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs), vp],
+        "tl_attn_rope_q8": [ctypes.POINTER(KvLayerQ8), ctypes.POINTER(AttnArgs),
+                            ctypes.POINTER(RopeParams), vp],
+        "tl_kv_append_rope_q8": [ctypes.POINTER(KvLayerQ8), vp, vp, u32, vp, u32, u32,
+                                 ctypes.POINTER(RopeParams), vp],
     }
     for name, args in sigs.items():
         f = getattr(L, name)
