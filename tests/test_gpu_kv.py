@@ -479,3 +479,43 @@ def test_append_layers_equals_per_layer(T, q8):
         assert T.equal(a.k, b.k) and T.equal(a.v, b.v)
         if q8:
             assert T.equal(a.ks, b.ks) and T.equal(a.vs, b.vs)
+
+
+def test_attn_rejects_bad_arguments_without_side_effects(T):
+    """Shapes the kernels do not support and positions past the cache are
+    rejected before any launch (TL_EINVAL / TL_ERANGE); an empty batch (n = 0)
+    is a no-op.  Neither touches the output or the cache."""
+    import tlkv
+    lib = tlkv.lib()
+    n_kv, hd, cap = 2, 128, 64
+    L = tlkv.Layer(cap, n_kv, hd)
+    L.k.fill_(1.0)
+    L.v.fill_(-2.0)
+    k0, v0 = L.k.clone(), L.v.clone()
+    rng = np.random.default_rng(3)
+    q = dev(T, rows(rng, 2, 32 * hd))
+    k = dev(T, rows(rng, 2, n_kv * hd))
+    out = T.full((2, 32 * hd), 7.0, dtype=T.float32, device="cuda")
+
+    def call(pos, n, n_head, window=0, qoff=0):
+        a = tlkv.attn_args(q, k, k, out, None, pos, n, n_head, hd, n_kv, window)
+        a.q = q.data_ptr() + qoff
+        return lib.tl_attn(L.desc, a, None)
+
+    TL_EINVAL, TL_ERANGE = -1, -2
+    assert call(10, 1, 3) == TL_EINVAL            # n_head not a multiple of n_kv
+    assert call(10, 1, 18) == TL_EINVAL           # gqa 9 > 8
+    assert call(10, 1, 8, qoff=4) == TL_EINVAL    # q not 16-byte aligned
+    assert call(cap - 1, 2, 8) == TL_ERANGE       # rows past the cache end
+    assert call(10, 0, 8) == 0                    # empty batch
+    sync(T)
+    assert bool((out == 7.0).all())
+    assert T.equal(L.k, k0) and T.equal(L.v, v0)
+    # a ring layer needs a window that fits it
+    R = tlkv.Layer(32, n_kv, hd, ring=32)
+    a = tlkv.attn_args(q, k, k, out, None, 40, 1, 8, hd, n_kv, 0)
+    assert lib.tl_attn(R.desc, a, None) == TL_EINVAL
+    a = tlkv.attn_args(q, k, k, out, None, 40, 2, 8, hd, n_kv, 32)
+    assert lib.tl_attn(R.desc, a, None) == TL_EINVAL   # window + n - 1 > ring
+    sync(T)
+    assert bool((out == 7.0).all())

@@ -9,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <type_traits>
+#include <utility>
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
@@ -212,6 +213,86 @@ struct RCfg {
  * probabilities stay <= 2^8 and most tiles skip the rescale. */
 #define TL_DEC_TAU 8.0f
 
+/* With G <= LPK every head of the group has its own lane in each key
+ * group, and the softmax of a tile runs once per (key pair, head) instead
+ * of once per lane: lane sub handles head sub and keeps that head's running
+ * sum in l[0]. */
+template <int G, int LPK>
+constexpr bool own_head_softmax() { return G <= LPK && LPK <= 16; }
+
+/* ds_swizzle in bit-mask mode (32-lane halves): every lane of an LPK-lane
+ * group reads lane H of its group. */
+template <int LPK, int H>
+TL_DEV u32 group_bcast(u32 v) {
+    return (u32)__builtin_amdgcn_ds_swizzle((int)v, (32 - LPK) | (H << 5));
+}
+template <int LPK, int G, int... H>
+TL_DEV void group_bcast_all(u32 (&pp)[G], u32 v, std::integer_sequence<int, H...>) {
+    ((pp[H] = group_bcast<LPK, H>(v)), ...);
+}
+
+/* Online-softmax step of one tile for the G heads of a lane's key pair:
+ * scores s0/s1 (identical across the LPK lanes of a key group) -> packed
+ * f16 probabilities pp[h].  The running max m[h] is common to the wave and
+ * moves only when a score exceeds it by more than TL_DEC_TAU (then l and
+ * acc are rescaled).  With own_head_softmax, lane sub computes the two
+ * probabilities of head sub only and the group reads them with one swizzle
+ * per head (2 exponentials per lane instead of 2G); l[0] then holds head
+ * sub's sum.  Otherwise every lane computes every head and l[h] holds head
+ * h's sum. */
+template <int G, int LPK>
+TL_DEV void tile_softmax(const float (&s0)[G], const float (&s1)[G], int sub, float (&m)[G],
+                         float (&l)[G], float (&acc)[G][16], u32 (&pp)[G]) {
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    if constexpr (own_head_softmax<G, LPK>()) {
+        float a0 = s0[0], a1 = s1[0], mo = m[0];
+#pragma unroll
+        for (int h = 1; h < G; h++)
+            if (sub == h) { a0 = s0[h]; a1 = s1[h]; mo = m[h]; }
+        if (__builtin_amdgcn_ballot_w64(sub < G && fmaxf(a0, a1) > mo + TL_DEC_TAU)) {
+            /* rare: move the wave's common max of each head that needs it */
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float mx = fmaxf(s0[h], s1[h]);
+                if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
+                    const float mn = group_max<64>(mx);
+                    const float alpha = fast_exp2(m[h] - mn);
+                    if (sub == h) l[0] *= alpha;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
+                    m[h] = mn;
+                }
+            }
+            mo = m[0];
+#pragma unroll
+            for (int h = 1; h < G; h++)
+                if (sub == h) mo = m[h];
+        }
+        const float mu = (mo == NEG_INF) ? 0.f : mo;
+        const float p0 = fast_exp2(a0 - mu), p1 = fast_exp2(a1 - mu);
+        l[0] += p0 + p1;
+        group_bcast_all<LPK, G>(pp, pack_f16x2_fast(p0, p1), std::make_integer_sequence<int, G>{});
+    } else {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float mx = fmaxf(s0[h], s1[h]);
+            if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
+                /* rare: move the wave's common max to this tile's max */
+                const float mn = group_max<64>(mx);
+                const float alpha = fast_exp2(m[h] - mn);
+                l[h] *= alpha;
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
+                m[h] = mn;
+            }
+            const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
+            const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
+            l[h] += p0 + p1;
+            pp[h] = pack_f16x2_fast(p0, p1);
+        }
+    }
+}
+
 /* Scores, online softmax and PV of one staged tile (keys tbase..tbase+TK-1,
  * those >= kend masked) into the lane group's running state (l, acc); the
  * running max m is common to the wave.  Logical
@@ -258,23 +339,7 @@ TL_DEV void ring_tile(const uint4 *tk, const uint4 *tv, const u32 (&qr)[G][8], u
     const uint4 va0 = tv[t0 * CPR + c0], va1 = tv[t0 * CPR + c1];
     const uint4 vb0 = tv[t1 * CPR + c0], vb1 = tv[t1 * CPR + c1];
     u32 pp[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float mx = fmaxf(s0[h], s1[h]);
-        if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
-            /* rare: move the wave's common max to this tile's max */
-            const float mn = group_max<64>(mx);
-            const float alpha = fast_exp2(m[h] - mn);
-            l[h] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
-            m[h] = mn;
-        }
-        const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
-        const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
-        l[h] += p0 + p1;
-        pp[h] = pack_f16x2_fast(p0, p1);
-    }
+    tile_softmax<G, LPK>(s0, s1, sub, m, l, acc, pp);
     const u32 va[8] = {va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
     const u32 vb[8] = {vb0.x, vb0.y, vb0.z, vb0.w, vb1.x, vb1.y, vb1.z, vb1.w};
 #pragma unroll
@@ -343,22 +408,7 @@ TL_DEV void ring_tile_q8(const uint4 *tk, const uint4 *tv, const u16 *sk, const 
     const uint4 va = tv[t0 * LPK + sub], vb = tv[t1 * LPK + sub];
     const u32 dvb = (u32)sv[t0 * NB + sub / 2] | ((u32)sv[t1 * NB + sub / 2] << 16);
     u32 pp[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float mx = fmaxf(s0[h], s1[h]);
-        if (__builtin_amdgcn_ballot_w64(mx > m[h] + TL_DEC_TAU)) {
-            const float mn = group_max<64>(mx);
-            const float alpha = fast_exp2(m[h] - mn);
-            l[h] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[h][e] *= alpha;
-            m[h] = mn;
-        }
-        const float mu = (m[h] == NEG_INF) ? 0.f : m[h];
-        const float p0 = fast_exp2(s0[h] - mu), p1 = fast_exp2(s1[h] - mu);
-        l[h] += p0 + p1;
-        pp[h] = pack_f16x2_fast(p0, p1);
-    }
+    tile_softmax<G, LPK>(s0, s1, sub, m, l, acc, pp);
     const half2_t dv2 = as_h2(dvb);                 /* (d of key t0, d of key t1) */
     const u32 vaw[4] = {va.x, va.y, va.z, va.w}, vbw[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
@@ -789,7 +839,11 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const int sub = lane % LPK, gi = lane / LPK;
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        if (sub == 0) s_lg[h][wave * GPW + gi] = l[h];
+        if constexpr (own_head_softmax<G, LPK>()) {
+            if (sub == h) s_lg[h][wave * GPW + gi] = l[0];
+        } else {
+            if (sub == 0) s_lg[h][wave * GPW + gi] = l[h];
+        }
         if (lane == 0) s_m[wave][h] = m[h];
     }
     const bool single = (n_split == 1);
