@@ -330,11 +330,13 @@ TL_DEV void ring_tile(const uint4 *tk, const uint4 *tv, const u32 (&qr)[G][8], u
          * each dot-product chain into its own divergent branch) */
         __asm__ volatile("" : "+v"(s0[h]), "+v"(s1[h]));
     }
-    const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
+    if (tbase + (u32)(2 * KPP) > kend) {   /* wave-uniform: only a chunk's last tile */
+        const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        s0[h] = v0 ? s0[h] : NEG_INF;
-        s1[h] = v1 ? s1[h] : NEG_INF;
+        for (int h = 0; h < G; h++) {
+            s0[h] = v0 ? s0[h] : NEG_INF;
+            s1[h] = v1 ? s1[h] : NEG_INF;
+        }
     }
     const uint4 va0 = tv[t0 * CPR + c0], va1 = tv[t0 * CPR + c1];
     const uint4 vb0 = tv[t1 * CPR + c0], vb1 = tv[t1 * CPR + c1];
@@ -399,11 +401,13 @@ TL_DEV void ring_tile_q8(const uint4 *tk, const uint4 *tv, const u16 *sk, const 
         s1[h] = group_sum<LPK>(s1[h]);
         __asm__ volatile("" : "+v"(s0[h]), "+v"(s1[h]));
     }
-    const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
+    if (tbase + (u32)(2 * KPP) > kend) {   /* wave-uniform: only a chunk's last tile */
+        const bool v0 = tbase + (u32)t0 < kend, v1 = tbase + (u32)t1 < kend;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        s0[h] = v0 ? s0[h] : NEG_INF;
-        s1[h] = v1 ? s1[h] : NEG_INF;
+        for (int h = 0; h < G; h++) {
+            s0[h] = v0 ? s0[h] : NEG_INF;
+            s1[h] = v1 ? s1[h] : NEG_INF;
+        }
     }
     const uint4 va = tv[t0 * LPK + sub], vb = tv[t1 * LPK + sub];
     const u32 dvb = (u32)sv[t0 * NB + sub / 2] | ((u32)sv[t1 * NB + sub / 2] << 16);
