@@ -133,6 +133,47 @@ def hbm_read_ceiling(torch, tlkv, lib, sh):
     return best
 
 
+def mfma_ceiling(torch, tlkv, lib, sh):
+    """Best dense f16 MFMA rate of a register-only v_mfma_f32_32x32x16_f16
+    loop (TFLOP/s): 2048 workgroups of 4 waves, 4 chains per wave."""
+    blocks, iters = 2048, 20000
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    flops = blocks * 4 * iters * 4 * 2 * 32 * 32 * 16
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    tlkv.check(lib.tl_probe_mfma(iters, blocks, tlkv.ptr(sink), sh))
+    best = 0.0
+    for _ in range(3):
+        e0.record()
+        tlkv.check(lib.tl_probe_mfma(iters, blocks, tlkv.ptr(sink), sh))
+        e1.record()
+        torch.cuda.synchronize()
+        best = max(best, flops / (e0.elapsed_time(e1) / 1e3) / 1e12)
+    del sink
+    return best
+
+
+def host_radix_cost(tlkv, n=32768, ub=512):
+    """The host prefix cache alone (libtlkv's kv_cache_*, C): config 4's
+    prefill bookkeeping -- a miss match, then kv_cache_append of n tokens in
+    ub-token chunks -- and a full-hit match of the same n tokens afterwards."""
+    toks = np.random.default_rng(4).integers(0, 128256, size=n, dtype=np.uint32)
+    C = tlkv.KvCache(n + 64)
+    t0 = time.perf_counter()
+    C.match(toks)
+    for p in range(0, n, ub):
+        if not C.append(toks, p, ub):
+            raise RuntimeError("kv_cache_append failed")
+    t1 = time.perf_counter()
+    hit = C.match(toks)
+    t2 = time.perf_counter()
+    C.close()
+    return {"append_ms": round((t1 - t0) * 1e3, 3),
+            "ns_per_token": round((t1 - t0) * 1e9 / n, 1),
+            "hit_match_ms": round((t2 - t1) * 1e3, 3), "hit_tokens": hit,
+            "note": f"{n} tokens in {ub}-token kv_cache_append calls (one host thread), "
+                    "then kv_cache_match of all of them"}
+
+
 # ---- the other BASELINE configs (reported beside the north star) -------------
 
 def _gbs(nbytes, ms):
@@ -637,6 +678,7 @@ def main():
     ev = lambda: torch.cuda.Event(enable_timing=True)
 
     ceiling = hbm_read_ceiling(torch, tlkv, lib, sh)
+    mfma_ceil = mfma_ceiling(torch, tlkv, lib, sh)
 
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0x9E3779B9 ^ 4)
@@ -816,6 +858,7 @@ def main():
                    "ctx": c["ctx"], "slots": 1},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "hbm_read_ceiling_GBs": round(ceiling, 1),
+        "host_radix": host_radix_cost(tlkv),
         "decode": {"us_per_layer_launch": round(avg_launch_us, 3),
                    "tok_s": round(K / (total_ms / 1e3), 1),
                    "frac_of_measured_ceiling": round(value / ceiling, 4)},
@@ -836,6 +879,8 @@ def main():
     if not args.no_prefill_attn:
         tf = pf_flops / (pf_ms / 1e3) / 1e12
         res["prefill"] = {"TFLOPs": round(tf, 2), "frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                          "mfma_ceiling_TFLOPs": round(mfma_ceil, 1),
+                          "frac_of_measured_mfma_ceiling": round(tf / mfma_ceil, 4),
                           "ms": round(pf_ms, 2), "flops": pf_flops,
                           "kernel": "attn_prefill_kernel<128,4> (+ split merge)"}
     del layers, slots, q, k, v, out

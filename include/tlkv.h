@@ -310,6 +310,12 @@ int tl_kv_append_rope_q8(const tl_kv_layer_q8 *L, const float *k, const float *v
 int tl_probe_read(const void *src, uint64_t bytes, uint32_t *sink,
                   uint32_t blocks, uint32_t depth, void *stream);
 
+/* Measurement aid (no reference counterpart): `blocks` workgroups of 256
+ * threads, each wave running `iters` x 4 v_mfma_f32_32x32x16_f16 (32768 flops
+ * each) on register operands; sink receives blocks*256 floats.  Gives the
+ * achievable dense f16 MFMA rate the prefill roofline is compared with. */
+int tl_probe_mfma(uint64_t iters, uint32_t blocks, float *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

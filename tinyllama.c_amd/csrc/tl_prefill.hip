@@ -123,3 +123,37 @@ int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &
     mp.ws_ml = p.ws_ml;
     return tl_launch_merge(mp, a->n, D, st);
 }
+
+/* ------------------------------------------------------------------------ */
+
+/* MFMA ceiling probe: every wave runs `iters` rounds of 4 independent
+ * v_mfma_f32_32x32x16_f16 chains on register operands (no memory traffic),
+ * then folds its accumulators into one word of `sink` so nothing is dead. */
+__global__ __launch_bounds__(256) void mfma_probe_kernel(u64 iters, float *sink) {
+    const int tid = threadIdx.x;
+    half8_t a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (_Float16)((float)((tid + i) & 7) * 0.125f);
+        b[i] = (_Float16)((float)((tid * 3 + i) & 7) * 0.0625f);
+    }
+    floatx16_t c[4] = {};
+    for (u64 it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c[j], 0, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) s += c[j][e];
+    sink[(u64)blockIdx.x * blockDim.x + tid] = s;
+}
+
+extern "C" int tl_probe_mfma(uint64_t iters, uint32_t blocks, float *sink, void *stream) {
+    if (!sink || blocks == 0 || iters == 0) return tl_fail(TL_EINVAL, "probe: bad arguments");
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (u64)iters,
+                       sink);
+    HIP_TRY(hipGetLastError());
+    return TL_OK;
+}

@@ -86,6 +86,7 @@ def lib():
         "tl_rope": [vp, u32, u32, u32, u32, u32, u32, ctypes.c_float,
                     ctypes.c_int, vp],
         "tl_probe_read": [vp, ctypes.c_uint64, vp, u32, u32, vp],
+        "tl_probe_mfma": [ctypes.c_uint64, u32, vp, vp],
         "tl_kv_append_layers": [ctypes.POINTER(KvLayer), u32, ctypes.POINTER(vp),
                                 ctypes.POINTER(vp), u32, vp, u32, u32, vp],
         "tl_kv_append_layers_q8": [ctypes.POINTER(KvLayerQ8), u32, ctypes.POINTER(vp),
