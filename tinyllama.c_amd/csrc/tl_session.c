@@ -94,7 +94,6 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
         }
     }
     if (cfg->use_radix) {
-        /* the prefix cache only stores the KvCache pointer */
         /* the prefix cache only stores the KvCache pointer; the session is
          * handed back to the state callbacks */
         s->radix = kv_cache_create((Session *)s,
