@@ -110,6 +110,20 @@ const char *tl_last_error(void);
 /* Select the device for the calling thread and set up library state. */
 int tl_init(int device);
 
+/* Launch-shape overrides (measurement and testing aid; no reference
+ * counterpart).  Every value defaults to 0 = automatic; the first library
+ * call reads the environment variable of the same name once (e.g.
+ * TL_DECODE_WGS=512), after which only tl_set_tuning changes them.
+ * Results do not depend on them beyond floating-point summation order. */
+#define TL_TUNE_DECODE_WGS          0   /* decode workgroups per launch */
+#define TL_TUNE_DECODE_MIN_KEYS     1   /* fewest keys per decode split */
+#define TL_TUNE_DECODE_MERGE_KERNEL 2   /* 1: merge decode splits in a separate launch */
+#define TL_TUNE_PREFILL_SPLITS      3   /* key splits of the prefill kernel */
+#define TL_TUNE_NO_PREFILL          4   /* 1: run every batch on the decode kernel */
+#define TL_TUNE_COUNT               5
+int tl_set_tuning(int key, uint32_t value);
+uint32_t tl_get_tuning(int key);
+
 /* Allocate / free one layer's K and V storage (hipMalloc, contents zero). */
 int tl_kv_layer_alloc(tl_kv_layer *L, uint32_t cap, uint32_t n_kv_head,
                       uint32_t head_dim, uint32_t ring);

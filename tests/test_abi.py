@@ -107,3 +107,16 @@ def test_executor_shim_loads():
     S = O.shim()
     for name in ("hip_graph_op", "hip_graph_op_set_slots", "hip_graph_op_set_stream"):
         assert hasattr(S, name)
+
+
+def test_tuning_overrides_need_no_device():
+    """Launch-shape overrides: set/get round trip, restore through the context
+    manager, unknown keys rejected."""
+    lib = tlkv.lib()
+    old = lib.tl_get_tuning(tlkv.TUNE_PREFILL_SPLITS)
+    with tlkv.tuning(tlkv.TUNE_PREFILL_SPLITS, 5):
+        assert lib.tl_get_tuning(tlkv.TUNE_PREFILL_SPLITS) == 5
+    assert lib.tl_get_tuning(tlkv.TUNE_PREFILL_SPLITS) == old
+    assert lib.tl_set_tuning(99, 1) == -1
+    assert lib.tl_set_tuning(-1, 1) == -1
+    assert lib.tl_get_tuning(99) == 0

@@ -6,7 +6,6 @@ Attention: within 2e-3 max-abs of the oracle's op_attn restatement, both over
 the same f16 cache (kernel error alone) and over the reference's f32 cache
 (the reference CPU semantics).
 """
-import os
 
 import numpy as np
 import pytest
@@ -284,12 +283,10 @@ def test_split_count_invariance(T):
     """The split-K decomposition does not change the result beyond rounding
     (p is rounded to f16 against each tile's running max)."""
     outs = []
-    for wgs in ("1", "64", "4096"):
-        os.environ["TL_DECODE_WGS"] = wgs
-        try:
+    import tlkv
+    for wgs in (1, 64, 4096):
+        with tlkv.tuning(tlkv.TUNE_DECODE_WGS, wgs):
             out, o16, _, _, _ = _run_attn(T, 32, 8, 128, 8192, 8000, 1, 0, None, seed=13)
-        finally:
-            del os.environ["TL_DECODE_WGS"]
         assert np.abs(out - o16).max() < TOL
         outs.append(out)
     assert np.abs(outs[0] - outs[1]).max() < 1e-4
@@ -303,15 +300,12 @@ def test_decode_variants_agree(T, shape):
     kernel: same result up to rounding, and each within tolerance of the
     oracle."""
     n_head, n_kv, hd, cap, pos = shape
+    import tlkv
     outs = []
-    for env in ({}, {"TL_DECODE_MERGE_KERNEL": "1"}):
-        os.environ.update(env)
-        try:
+    for merge_kernel in (0, 1):
+        with tlkv.tuning(tlkv.TUNE_DECODE_MERGE_KERNEL, merge_kernel):
             out, o16, _, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, 1, 0, None, seed=pos)
-        finally:
-            for k in env:
-                del os.environ[k]
-        assert np.abs(out - o16).max() < TOL, env
+        assert np.abs(out - o16).max() < TOL, merge_kernel
         outs.append(out)
     for o in outs[1:]:
         assert np.abs(outs[0] - o).max() < 1e-4
@@ -394,12 +388,10 @@ def test_prefill_vs_oracle(T, case):
 
 def test_prefill_split_invariance(T):
     outs = []
-    for ns in ("1", "3", "7"):
-        os.environ["TL_PREFILL_SPLITS"] = ns
-        try:
+    import tlkv
+    for ns in (1, 3, 7):
+        with tlkv.tuning(tlkv.TUNE_PREFILL_SPLITS, ns):
             out, o16, _, _, _ = _run_attn(T, 32, 8, 128, 2100, 1500, 512, 0, None, seed=21)
-        finally:
-            del os.environ["TL_PREFILL_SPLITS"]
         assert np.abs(out - o16).max() < TOL
         outs.append(out)
     assert np.abs(outs[0] - outs[1]).max() < 1e-4

@@ -220,17 +220,14 @@ def test_attn_q8_full_size_config4(T):
 
 def test_attn_q8_split_invariance(T):
     """Different split counts (decode workgroups) give results within rounding."""
-    import os
+    import tlkv
     rng = np.random.default_rng(9)
     cap = 6000
     slots = rng.permutation(cap).astype(np.uint32)
     outs = []
-    for wgs in ("8", "64", ""):
-        os.environ["TL_DECODE_WGS"] = wgs
-        try:
+    for wgs in (8, 64, 0):
+        with tlkv.tuning(tlkv.TUNE_DECODE_WGS, wgs):
             out, ref, _, _ = _run_attn_q8(T, 32, 8, 128, cap, 5900, 1, 0, slots, seed=3)
-        finally:
-            os.environ.pop("TL_DECODE_WGS", None)
         assert np.abs(out - ref).max() < TOL, wgs
         outs.append(out)
     assert np.abs(outs[0] - outs[2]).max() < 1e-3

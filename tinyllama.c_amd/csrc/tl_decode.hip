@@ -54,10 +54,10 @@ static DecKernel pick_kernel(int G, bool rope, bool q8) {
     }
 }
 
-static u32 env_u32(const char *name, u32 dflt) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    return (u32)strtoul(s, NULL, 10);
+/* override `key` when set, else the automatic value */
+static u32 tuned(int key, u32 dflt) {
+    const u32 v = tl_tune(key);
+    return v ? v : dflt;
 }
 
 static int cu_count() {
@@ -113,14 +113,14 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
      * (one resident wave of workgroups; more per CU only shortens chunks) */
     int per_cu = resident_per_cu(K.fn, K.threads);
     if (per_cu > 2) per_cu = 2;
-    const u32 target = env_u32("TL_DECODE_WGS", (u32)(per_cu * cu_count()));
+    const u32 target = tuned(TL_TUNE_DECODE_WGS, (u32)(per_cu * cu_count()));
     const u64 n_groups = (u64)n_rows_total * p.n_kv;
     u32 n_split = (u32)((target + n_groups - 1) / n_groups);
     const u32 waves = (u32)K.threads / 64;
     /* keys per split: one tile per wave, at most 128 (head_dim 64, P = 700:
      * 128 keys per split 8.8 us vs 9.5 us at 256; fewer keys make the
      * merge dearer than the shorter chunks save) */
-    const u32 min_keys = env_u32("TL_DECODE_MIN_KEYS", waves * tk < 128 ? waves * tk : 128);
+    const u32 min_keys = tuned(TL_TUNE_DECODE_MIN_KEYS, waves * tk < 128 ? waves * tk : 128);
     const u32 max_split = (max_vis + min_keys - 1) / min_keys;
     const u32 min_split = (max_vis + TL_DEC_MAX_CHUNK - 1) / TL_DEC_MAX_CHUNK;
     if (n_split > max_split) n_split = max_split;
@@ -134,7 +134,7 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     p.n_split = n_split;
     p.counters = nullptr;
     const bool in_kernel_merge = n_split > 1 && G * n_split <= 2048 &&
-                                 !env_u32("TL_DECODE_MERGE_KERNEL", 0);
+                                 !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL);
     if (n_split > 1) {
         TlWorkspace *w;
         size_t parts = (size_t)n_rows_total * p.n_head * n_split;

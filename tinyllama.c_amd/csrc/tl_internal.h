@@ -95,6 +95,9 @@ int tl_rope_cfg(uint32_t head_dim, const tl_rope_params *r, RopeCfg &c);
 
 int tl_fail(int code, const char *fmt, ...);
 
+/* launch-shape override `key` (TL_TUNE_*), 0 = automatic */
+uint32_t tl_tune(int key);
+
 #define HIP_TRY(expr)                                                         \
     do {                                                                      \
         hipError_t e_ = (expr);                                               \

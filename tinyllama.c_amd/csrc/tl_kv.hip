@@ -19,6 +19,8 @@
 #include "tl_internal.h"
 #include "../../include/tlkv.h"
 
+#include <atomic>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -90,6 +92,37 @@ extern "C" int tl_init(int device) {
     TlWorkspace *w;
     return tl_workspace_get(1 << 20, 1 << 14, 4096, &w);
 }
+
+/* launch-shape overrides: seeded once from the environment, then only
+ * tl_set_tuning writes them (relaxed atomics: a launch reads a consistent
+ * word, and callers that change them between launches order the change
+ * themselves) */
+static std::atomic<u32> g_tune[TL_TUNE_COUNT];
+static std::once_flag g_tune_once;
+
+static void tune_seed() {
+    static const char *const names[TL_TUNE_COUNT] = {
+        "TL_DECODE_WGS", "TL_DECODE_MIN_KEYS", "TL_DECODE_MERGE_KERNEL", "TL_PREFILL_SPLITS",
+        "TL_NO_PREFILL"};
+    for (int i = 0; i < TL_TUNE_COUNT; i++) {
+        const char *e = getenv(names[i]);
+        g_tune[i].store(e && *e ? (u32)strtoul(e, NULL, 10) : 0u, std::memory_order_relaxed);
+    }
+}
+
+uint32_t tl_tune(int key) {
+    std::call_once(g_tune_once, tune_seed);
+    return (key >= 0 && key < TL_TUNE_COUNT) ? g_tune[key].load(std::memory_order_relaxed) : 0u;
+}
+
+extern "C" int tl_set_tuning(int key, uint32_t value) {
+    if (key < 0 || key >= TL_TUNE_COUNT) return tl_fail(TL_EINVAL, "tuning key %d", key);
+    std::call_once(g_tune_once, tune_seed);
+    g_tune[key].store(value, std::memory_order_relaxed);
+    return TL_OK;
+}
+
+extern "C" uint32_t tl_get_tuning(int key) { return tl_tune(key); }
 
 /* ------------------------------------------------------------------------ */
 /* layer storage                                                             */

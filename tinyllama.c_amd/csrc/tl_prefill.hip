@@ -42,7 +42,7 @@ TL_PREFILL_PICKER(tl_prefill_fn, false, false)
 /* ------------------------------------------------------------------------ */
 
 bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a) {
-    if (getenv("TL_NO_PREFILL")) return false;
+    if (tl_tune(TL_TUNE_NO_PREFILL)) return false;
     const u32 G = a->n_head / L.n_kv_head;
     return (L.head_dim == 64 || L.head_dim == 128 || L.head_dim == 256) && G >= 1 && G <= 8;
 }
@@ -92,7 +92,7 @@ int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &
     const u32 max_ns = (span + 511) / 512;  /* keep >= 512 keys per split */
     if (ns > max_ns) ns = max_ns;
     if (ns < 1) ns = 1;
-    if (const char *e = getenv("TL_PREFILL_SPLITS")) ns = (u32)atoi(e) ? (u32)atoi(e) : ns;
+    if (const u32 t = tl_tune(TL_TUNE_PREFILL_SPLITS)) ns = t;
     p.n_split = ns;
     if (ns > 1) {
         TlWorkspace *w;

@@ -54,6 +54,28 @@ class TlError(RuntimeError):
     pass
 
 
+# launch-shape overrides (include/tlkv.h TL_TUNE_*)
+TUNE_DECODE_WGS, TUNE_DECODE_MIN_KEYS, TUNE_DECODE_MERGE_KERNEL = 0, 1, 2
+TUNE_PREFILL_SPLITS, TUNE_NO_PREFILL = 3, 4
+
+
+class tuning:
+    """Context manager: set a TL_TUNE_* override, restore the old value on exit."""
+
+    def __init__(self, key, value):
+        self.key, self.value = key, int(value)
+
+    def __enter__(self):
+        L = lib()
+        self.old = int(L.tl_get_tuning(self.key))
+        check(L.tl_set_tuning(self.key, self.value))
+        return self
+
+    def __exit__(self, *exc):
+        check(lib().tl_set_tuning(self.key, self.old))
+        return False
+
+
 def lib():
     """Load libtlkv.so once (raises if it was not built)."""
     global _lib
@@ -87,6 +109,8 @@ def lib():
                     ctypes.c_int, vp],
         "tl_probe_read": [vp, ctypes.c_uint64, vp, u32, u32, vp],
         "tl_probe_mfma": [ctypes.c_uint64, u32, vp, vp],
+        "tl_set_tuning": [ctypes.c_int, u32],
+        "tl_get_tuning": [ctypes.c_int],
         "tl_kv_append_layers": [ctypes.POINTER(KvLayer), u32, ctypes.POINTER(vp),
                                 ctypes.POINTER(vp), u32, vp, u32, u32, vp],
         "tl_kv_append_layers_q8": [ctypes.POINTER(KvLayerQ8), u32, ctypes.POINTER(vp),
@@ -112,6 +136,7 @@ def lib():
         f = getattr(L, name)
         f.argtypes = args
         f.restype = ctypes.c_int
+    L.tl_get_tuning.restype = u32
     _lib = L
     return L
 
