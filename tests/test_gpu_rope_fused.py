@@ -43,6 +43,8 @@ CASES = [
     (16, 2, 128, 300, 5, 64, 1, 1e4),        # multi-row decode, partial rope_dim
     (32, 8, 128, 1000, 100, 128, 0, 5e5),    # prefill batch (append + MFMA kernel)
     (8, 4, 64, 200, 40, 32, 0, 1e4),         # prefill, head_dim 64, partial NORM
+    (32, 8, 64, 700, 1, 64, 0, 5e5),         # decode, head_dim 64 (config 1 shape)
+    (8, 4, 256, 600, 64, 256, 1, 1e6),       # prefill, head_dim 256, NEOX (config 5 global)
 ]
 
 
