@@ -99,6 +99,41 @@ def cpu_baseline(c, P, n_layers_sample):
                       f"the f16 workload's algorithmic bytes"}
 
 
+def cpu_baseline_sessions(c, P, n_sessions, calls):
+    """The reference op_attn for `n_sessions` concurrent sessions, one host
+    thread each (the CPU server's -np N), `calls` decode-layer calls per
+    session at P keys; aggregate GB/s of the f16 workload's algorithmic bytes
+    over the wall time of the parallel section (ctypes releases the GIL)."""
+    import oracle as O
+    from concurrent.futures import ThreadPoolExecutor
+    if not O.ref_available():
+        return None
+    kd = c["Hkv"] * c["d"]
+    slots = np.arange(P, dtype=np.uint32)
+    data = []
+    for i in range(n_sessions):
+        rng = np.random.default_rng(100 + i)
+        data.append((rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32),
+                     rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32),
+                     rng.standard_normal((calls, c["Hq"] * c["d"]), dtype=np.float32),
+                     rng.standard_normal((calls, kd), dtype=np.float32)))
+
+    def work(i):
+        kc, vc, q, k = data[i]
+        for j in range(calls):
+            O.ref_attn(kc, vc, q[j:j + 1], k[j:j + 1], k[j:j + 1], slots, P - 1, 1, c["Hq"])
+
+    with ThreadPoolExecutor(n_sessions) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(work, range(n_sessions)))
+        secs = time.perf_counter() - t0
+    gbs = n_sessions * calls * decode_bytes(c, P) / secs / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": n_sessions, "kind": "reference",
+            "sample": f"{n_sessions} sessions on {n_sessions} threads, {calls} decode-layer "
+                      f"op_attn calls each at P={P} (f32 cache; {os.cpu_count()} host cores "
+                      f"present), {secs * 1e3:.0f} ms wall"}
+
+
 def profiled_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (profiles/attn_decode_llama3-8b-32k_hbm_traffic.md)."""
@@ -899,6 +934,9 @@ def main():
         res["other_configs"] = others
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(c, c["ctx"] + 1, args.cpu_layers)
+        if "config2" in others:
+            c2 = dict(Hq=28, Hkv=4, d=128)
+            others["config2"]["cpu_baseline"] = cpu_baseline_sessions(c2, 8193, 8, 28)
     print(json.dumps(res), flush=True)
 
 
