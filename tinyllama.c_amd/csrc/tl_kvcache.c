@@ -345,9 +345,20 @@ u32 kv_cache_match(KvRadixCache *c, const u32 *tokens, u32 n) {
 /* trie node of tokens[0..len): from the cursor when it still describes that
  * prefix, else by walking from the root (TL_TRIE_NONE if absent) */
 static u32 prefix_node(KvRadixCache *c, const u32 *tokens, u32 len) {
-    if (c->cur_valid && c->cur_epoch == c->trie.epoch && c->cur_len == len &&
-        memcmp(c->cur_key, tokens, (size_t)len * sizeof(u32)) == 0)
-        return c->cur_node;
+    if (c->cur_valid && c->cur_len == len &&
+        memcmp(c->cur_key, tokens, (size_t)len * sizeof(u32)) == 0) {
+        if (c->cur_epoch == c->trie.epoch || len == 0) return c->cur_node;
+        /* nodes were pruned since: the cursor still stands when it is the
+         * node of the request's slot for position len - 1.  That slot is
+         * pinned by the request (ref_count >= 1), so its key -- and the node
+         * holding it -- cannot have been evicted. */
+        if (len <= c->req.len) {
+            const u32 s = c->req.slots[len - 1];
+            if (s < c->pool.n_slots && c->meta[s].in_tree && c->meta[s].ref_count > 0 &&
+                c->node_of[s] == c->cur_node)
+                return c->cur_node;
+        }
+    }
     return tl_trie_walk(&c->trie, TL_TRIE_ROOT, tokens, len);
 }
 
@@ -363,8 +374,8 @@ bool kv_cache_append(KvRadixCache *c, const u32 *tokens, u32 pos, u32 n) {
     if (!c || !c->enabled || n == 0) return true;
     if ((u64)pos + n > c->ctx_size) return false;
 
-    c->cur_valid = false;
     u32 node = prefix_node(c, tokens, pos);
+    c->cur_valid = false;   /* set again below once the new prefix is in */
     for (u32 k = 0; k < n; k++) {
         const u32 i = pos + k;
         if (i < c->req.len) {
