@@ -66,9 +66,11 @@ int  tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens
                         uint32_t q_stride, uint32_t kv_stride);
 
 /* tl_session_execute without the attention: the chunk loop's
- * kv_cache_append + slot upload + K/V write-through (the part of OP_ATTN at
- * src/backend/cpu/cpu_op.c:995-1008) for every layer.  For callers that fill
- * or extend a cache whose attention outputs they do not need. */
+ * kv_cache_append calls (per n_ubatch chunk, as graph_execute makes them),
+ * then one slot upload and the K/V write-through (the part of OP_ATTN at
+ * src/backend/cpu/cpu_op.c:995-1008) of the whole batch for every layer.
+ * For callers that fill or extend a cache whose attention outputs they do
+ * not need. */
 int  tl_session_append(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                        const float *const *k, const float *const *v, uint32_t kv_stride);
 

@@ -210,3 +210,73 @@ def test_session_fork_from_donor(T):
     b, _ = _cached_rows(T, S, n_layer, 160)
     for path, rows in a.items():
         assert b[path] == rows
+
+
+@pytest.mark.parametrize("kv_q8", [False, True])
+def test_session_append_only_multi_chunk(T, kv_q8):
+    """tl_session_append: the prefix cache takes every n_ubatch chunk of a
+    batch, then one slot upload and one write-through cover the batch.  With
+    prefix reuse and LRU eviction (a pool of 96 rows, batches of up to 70
+    tokens in 16-token chunks), the rows behind every request's slot map are
+    the f16 (or Q8_0) conversion of that request's own rows, bit for bit, and
+    the host trace equals a chunk-by-chunk replay through kv_cache_append."""
+    import tlkv
+    n_layer, nkv, hd, ctx, ub = 2, 2, 64, 96, 16
+    kd = nkv * hd
+    S = tlkv.Session(n_layer, 8, nkv, hd, ctx, ub, kv_q8=kv_q8)
+    ref = tlkv.KvCache(ctx)                      # the same calls, host only
+    rng = np.random.default_rng(31)
+    shared = [list(rng.integers(0, 1000, size=n)) for n in (23, 40)]
+    for i in range(8):
+        toks = shared[i % 2] + list(rng.integers(0, 1000, size=int(rng.integers(5, 31))))
+        arr = np.array(toks, np.uint32)
+        m, resume = S.kv_prepare(arr)
+        assert ref.match(arr) == m
+        n = len(toks) - resume
+        k = [T.from_numpy(np.stack([prefix_rows(toks, p, kd, b"k%d" % l)
+                                    for p in range(resume, len(toks))])).cuda()
+             for l in range(n_layer)]
+        v = [T.from_numpy(np.stack([prefix_rows(toks, p, kd, b"v%d" % l)
+                                    for p in range(resume, len(toks))])).cuda()
+             for l in range(n_layer)]
+        S.append(arr[resume:], k, v, kd)
+        for p0 in range(resume, len(toks), ub):
+            assert ref.append(arr, p0, min(ub, len(toks) - p0))
+        T.cuda.synchronize()
+        slots = S.radix_slots(len(toks))
+        assert np.array_equal(slots, ref.slots(len(toks)))
+        for l in range(n_layer):
+            allk = np.stack([prefix_rows(toks, p, kd, b"k%d" % l) for p in range(len(toks))])
+            allv = np.stack([prefix_rows(toks, p, kd, b"v%d" % l) for p in range(len(toks))])
+            sl = T.tensor(slots.astype(np.int32), device="cuda")
+            if kv_q8:
+                lay = S.layer_q8(l)
+                ko = T.zeros((len(toks), nkv, hd), dtype=T.int8, device="cuda")
+                vo = T.zeros_like(ko)
+                kso = T.zeros((len(toks), nkv, hd // 32), dtype=T.int16, device="cuda")
+                vso = T.zeros_like(kso)
+                tlkv.check(tlkv.lib().tl_kv_gather_q8(lay, tlkv.ptr(sl), len(toks), tlkv.ptr(ko),
+                                                      tlkv.ptr(kso), tlkv.ptr(vo), tlkv.ptr(vso),
+                                                      None))
+                T.cuda.synchronize()
+                qk, dk = O.q8_quantize(allk.reshape(len(toks), nkv, hd))
+                qv, dv = O.q8_quantize(allv.reshape(len(toks), nkv, hd))
+                assert np.array_equal(ko.cpu().numpy(), qk)
+                assert np.array_equal(kso.cpu().numpy().view(np.uint16), dk)
+                assert np.array_equal(vo.cpu().numpy(), qv)
+                assert np.array_equal(vso.cpu().numpy().view(np.uint16), dv)
+            else:
+                lay = S.layer(l)
+                ko = T.zeros((len(toks), nkv, hd), dtype=T.float16, device="cuda")
+                vo = T.zeros_like(ko)
+                tlkv.check(tlkv.lib().tl_kv_gather(lay, tlkv.ptr(sl), len(toks), tlkv.ptr(ko),
+                                                   tlkv.ptr(vo), None))
+                T.cuda.synchronize()
+                assert np.array_equal(ko.cpu().numpy().view(np.uint16).reshape(len(toks), -1),
+                                      O.f16_bits(allk))
+                assert np.array_equal(vo.cpu().numpy().view(np.uint16).reshape(len(toks), -1),
+                                      O.f16_bits(allv))
+    st = tlkv._kv_sigs().tl_kv_cache_stats(S.radix).contents
+    assert (st.hit_tokens, st.evictions, st.allocations) == (
+        ref.stats()["hit_tokens"], ref.stats()["evictions"], ref.stats()["allocations"])
+    assert st.evictions > 0

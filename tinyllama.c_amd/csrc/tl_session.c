@@ -199,7 +199,48 @@ int tl_session_kv_prepare(tl_session *s, const uint32_t *tokens, uint32_t n,
     return TL_OK;
 }
 
-/* The chunk loop of graph_execute; q == NULL runs the K/V write-through only. */
+/* K/V write-through only (no attention): the prefix cache takes every
+ * n_ubatch chunk of the batch first -- the same kv_cache_append calls, in the
+ * same order, as the chunk loop below makes -- then one slot-table upload and
+ * one write-through launch per 16 layers cover the whole batch.  No chunk's
+ * rows can be evicted by a later chunk: the request pins its slots. */
+static int append_only(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
+                       const float *const *k, const float *const *v, uint32_t kv_stride) {
+    const uint32_t pos = s->n_tokens;
+    if ((uint64_t)pos + n_tokens > s->cfg.ctx_size)
+        return fail(TL_ERANGE, "append: batch exceeds ctx_size");
+    memcpy(s->tokens + pos, tokens, (size_t)n_tokens * sizeof(uint32_t));
+    if (s->radix) {
+        for (uint32_t done = 0; done < n_tokens;) {
+            uint32_t chunk = n_tokens - done;
+            if (chunk > s->cfg.n_ubatch) chunk = s->cfg.n_ubatch;
+            if (!kv_cache_append(s->radix, s->tokens, pos + done, chunk))
+                return fail(TL_ERANGE, "KV slot allocation failed");
+            done += chunk;
+        }
+        const KvRequestState *req = tl_kv_cache_req(s->radix);
+        if (req->len < pos + n_tokens) return fail(TL_ERANGE, "append: request map too short");
+        uint32_t lo = tl_kv_cache_take_dirty(s->radix);
+        if (lo != KV_SLOT_NONE && lo < pos + n_tokens) {
+            int rc = upload_slots(s, lo, pos + n_tokens);
+            if (rc) return rc;
+        }
+    }
+    const uint32_t *sl = s->radix ? s->d_slots : NULL;
+    for (uint32_t l0 = 0; l0 < s->cfg.n_layer; l0 += 64) {
+        const uint32_t nl = s->cfg.n_layer - l0 < 64 ? s->cfg.n_layer - l0 : 64;
+        int rc = s->layers8
+                     ? tl_kv_append_layers_q8(&s->layers8[l0], nl, k + l0, v + l0, kv_stride, sl,
+                                              pos, n_tokens, s->cfg.stream)
+                     : tl_kv_append_layers(&s->layers[l0], nl, k + l0, v + l0, kv_stride, sl,
+                                           pos, n_tokens, s->cfg.stream);
+        if (rc) return rc;
+    }
+    s->n_tokens = pos + n_tokens;
+    return TL_OK;
+}
+
+/* The chunk loop of graph_execute (src/graph.c:1395-1413). */
 static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                       const float *const *q, const float *const *k,
                       const float *const *v, float *const *out,
@@ -224,26 +265,7 @@ static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                 if (rc) return rc;
             }
         }
-        if (!q) {
-            /* write-through only: every layer's rows of the chunk, batched
-             * into one launch per 16 layers */
-            const float *kl[64], *vl[64];
-            const uint32_t *sl = s->radix ? s->d_slots : NULL;
-            for (uint32_t l0 = 0; l0 < s->cfg.n_layer; l0 += 64) {
-                const uint32_t nl = s->cfg.n_layer - l0 < 64 ? s->cfg.n_layer - l0 : 64;
-                for (uint32_t j = 0; j < nl; j++) {
-                    kl[j] = k[l0 + j] + (size_t)done * kv_stride;
-                    vl[j] = v[l0 + j] + (size_t)done * kv_stride;
-                }
-                int rc = s->layers8
-                             ? tl_kv_append_layers_q8(&s->layers8[l0], nl, kl, vl, kv_stride, sl,
-                                                      p0, chunk, s->cfg.stream)
-                             : tl_kv_append_layers(&s->layers[l0], nl, kl, vl, kv_stride, sl, p0,
-                                                   chunk, s->cfg.stream);
-                if (rc) return rc;
-            }
-        }
-        for (uint32_t l = 0; l < s->cfg.n_layer && q; l++) {
+        for (uint32_t l = 0; l < s->cfg.n_layer; l++) {
             tl_attn_args a;
             memset(&a, 0, sizeof(a));
             a.q = q[l] + (size_t)done * q_stride;
@@ -281,7 +303,7 @@ int tl_session_append(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                       const float *const *k, const float *const *v, uint32_t kv_stride) {
     if (!s || !tokens || n_tokens == 0) return fail(TL_EINVAL, "append: missing tokens");
     if (!k || !v) return fail(TL_EINVAL, "append: missing activations");
-    return run_chunks(s, tokens, n_tokens, NULL, k, v, NULL, 0, kv_stride);
+    return append_only(s, tokens, n_tokens, k, v, kv_stride);
 }
 
 /* Compaction: optional LRU trim, then renumber the pool so live rows occupy
