@@ -24,7 +24,7 @@ struct tl_session {
     uint32_t      *tokens;      /* [ctx_size] host token history (Session.tokens) */
     uint32_t       n_tokens;    /* Session.n_tokens */
     uint32_t      *d_slots;     /* device mirror of req.slots */
-    uint32_t      *d_moves;     /* device [2 * ctx_size]: copy sources, destinations */
+    uint32_t      *d_moves;     /* device [2 * ctx_size]: n copy sources, then n destinations */
     uint32_t      *h_moves;     /* host   [2 * ctx_size] */
     uint32_t      *stage;       /* pinned */
     uint32_t       stage_pos;
@@ -320,12 +320,13 @@ int tl_session_compact(tl_session *s, uint32_t keep, uint32_t *evicted, uint32_t
     uint32_t n = tl_kv_cache_compact(s->radix, src, dst, ctx);
     if (n == UINT32_MAX) return fail(TL_ERANGE, "compact: move list overflow");
     if (n) {
-        int rc = upload_words(s, s->d_moves, src, n);
-        if (!rc) rc = upload_words(s, s->d_moves + ctx, dst, n);
+        /* sources then destinations, packed: one upload */
+        memmove(src + n, dst, (size_t)n * sizeof(uint32_t));
+        int rc = upload_words(s, s->d_moves, src, 2 * n);
         if (!rc)
             rc = s->layers8 ? tl_kv_copy_q8(s->layers8, s->cfg.n_layer, s->d_moves,
-                                            s->d_moves + ctx, n, s->cfg.stream)
-                            : tl_kv_copy(s->layers, s->cfg.n_layer, s->d_moves, s->d_moves + ctx,
+                                            s->d_moves + n, n, s->cfg.stream)
+                            : tl_kv_copy(s->layers, s->cfg.n_layer, s->d_moves, s->d_moves + n,
                                          n, s->cfg.stream);
         if (!rc) rc = sync_slots(s);
         if (rc) return rc;
@@ -354,7 +355,7 @@ int tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t 
         return fail(TL_EINVAL, "fork: sessions differ in shape or cache type");
     const uint32_t ctx = s->cfg.ctx_size;
     uint32_t m = kv_cache_match(s->radix, tokens, n);
-    uint32_t *src = s->h_moves, *dst = s->h_moves + ctx;
+    uint32_t *src = s->h_moves;
     uint32_t lim = n < ctx ? n : ctx;
     uint32_t md = tl_kv_cache_lookup(donor->radix, tokens, lim, src);
     if (md > m) {
@@ -362,14 +363,16 @@ int tl_session_kv_prepare_from(tl_session *s, tl_session *donor, const uint32_t 
         if (!kv_cache_append(s->radix, tokens, m, nc)) return fail(TL_ERANGE, "fork: KV slot allocation failed");
         const KvRequestState *req = tl_kv_cache_req(s->radix);
         if (req->len < md) return fail(TL_ERANGE, "fork: request map too short");
-        memcpy(dst, req->slots + m, (size_t)nc * sizeof(uint32_t));
-        int rc = upload_words(s, s->d_moves, src + m, nc);
-        if (!rc) rc = upload_words(s, s->d_moves + ctx, dst, nc);
+        /* sources (donor rows) then destinations, packed at the front of
+         * h_moves ([0, 2 nc), nc <= ctx): one upload */
+        memmove(src, src + m, (size_t)nc * sizeof(uint32_t));
+        memcpy(src + nc, req->slots + m, (size_t)nc * sizeof(uint32_t));
+        int rc = upload_words(s, s->d_moves, src, 2 * nc);
         if (!rc)
             rc = s->layers8 ? tl_kv_copy_between_q8(s->layers8, donor->layers8, s->cfg.n_layer,
-                                                    s->d_moves, s->d_moves + ctx, nc, s->cfg.stream)
+                                                    s->d_moves, s->d_moves + nc, nc, s->cfg.stream)
                             : tl_kv_copy_between(s->layers, donor->layers, s->cfg.n_layer,
-                                                 s->d_moves, s->d_moves + ctx, nc, s->cfg.stream);
+                                                 s->d_moves, s->d_moves + nc, nc, s->cfg.stream);
         if (!rc) rc = sync_slots(s);
         if (rc) return rc;
         if (forked) *forked = nc;
