@@ -158,7 +158,7 @@ int tl_kv_copy_between(const tl_kv_layer *dst_layers, const tl_kv_layer *src_lay
                        uint32_t n_layer, const uint32_t *src, const uint32_t *dst,
                        uint32_t n, void *stream);
 
-/* Fused RoPE + OP_ATTN (SURVEY-listed next step "fused RoPE + append"; the
+/* Fused RoPE + OP_ATTN (the reference's own to-do, REMEMBER.md:20; the
  * reference runs OP_ROPE on Q and K, cpu_op.c:637-700, then OP_ATTN,
  * cpu_op.c:964-1064).  Same results as tl_rope(q rows at pos..), tl_rope(k
  * rows at pos..) then tl_attn, bit for bit, in one launch for decode batches
