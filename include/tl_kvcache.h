@@ -22,8 +22,9 @@
  * on random request streams).  The prefix index is a token trie instead of
  * the vendored rax; eviction picks the same victim (the in-tree leaf with
  * ref_count 0 and the smallest last_used) from a heap instead of a full scan.
- * Session and KvCache are opaque here: kv_cache_create only keeps the
- * pointers; state snapshots go through the callbacks set with
+ * The struct's leading fields (through req and enabled) sit at the
+ * reference's offsets (TlKvRadixHead below).  Session and KvCache are opaque
+ * here: kv_cache_create only keeps the pointers; state snapshots go through the callbacks set with
  * tl_kv_cache_set_state_ops (none set = no snapshots, as for a Session whose
  * graph has no recurrent state).
  */
@@ -99,6 +100,25 @@ typedef struct {
 } TlKvStateOps;
 
 typedef struct KvRadixCache KvRadixCache;
+
+/* The leading fields of struct KvRadixCache, in the reference's order and at
+ * its offsets (src/kvcache.h:50-57).  op_attn reads radix->req.slots and
+ * radix->req.len straight from the struct (src/backend/cpu/cpu_op.c:988-993),
+ * and so does any code compiled against the reference's kvcache.h, so a
+ * KvRadixCache made by this library may be handed to such code as the
+ * reference's own.  Fields past `enabled` are private and differ.  `tree`
+ * points to this library's trie, not to a rax; `n_layer` is 0 (KvCache is
+ * opaque here).  Read-only for callers: the library owns every field. */
+typedef struct {
+    void          *tree;
+    KvSlotPool     pool;
+    KvSlotMeta    *meta;
+    KvRequestState req;
+    KvCache       *kv;
+    u32            n_layer;
+    u32            ctx_size;
+    bool           enabled;
+} TlKvRadixHead;
 
 KvRadixCache *kv_cache_create(Session *s, KvCache *kv, u32 ctx_size);
 void kv_cache_destroy(KvRadixCache *c);

@@ -83,6 +83,10 @@ def ref():
         R.rh_attn.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32, _vp,
                               _u32, _u32, _u32, _u32, _u32, _u32, _u32]
         R.rh_attn.restype = ctypes.c_int
+        R.rh_attn_radix.argtypes = [_vp, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _u32,
+                                    _u32, _u32, _u32, _u32, _u32, _u32]
+        R.rh_attn_radix.restype = ctypes.c_int
+        R.rh_radix_layout.argtypes = [_u64p]
         R.rh_rope.argtypes = [ctypes.c_int, _f32p, _f32p, _u32, _u32, _u32, _u32,
                               _u32, _u32, ctypes.c_float]
         R.rh_rope.restype = ctypes.c_int
@@ -91,6 +95,8 @@ def ref():
         R.rh_kv_destroy.argtypes = [_vp]
         R.rh_kv_match.argtypes = [_vp, _u32p, _u32]
         R.rh_kv_match.restype = _u32
+        R.rh_kv_lookup.argtypes = [_vp, _u32p, _u32]
+        R.rh_kv_lookup.restype = _u32
         R.rh_kv_append.argtypes = [_vp, _u32p, _u32, _u32]
         R.rh_kv_append.restype = ctypes.c_int
         R.rh_kv_req.argtypes = [_vp, _u32p]
@@ -126,9 +132,18 @@ def shim():
     global _shim
     if _shim is None and os.path.exists(SHIM_SO):
         S = ctypes.CDLL(SHIM_SO)
-        S.rh_attn_shim.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _u32, _u32,
+        S.rh_attn_shim.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32,
                                    _u32, _u32, _u32, _u32, _vp]
         S.rh_attn_shim.restype = ctypes.c_int
+        S.rh_layer_shim.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32,
+                                    _u32, _u32, _u32, _u32, _u32, ctypes.c_int,
+                                    ctypes.c_float, _u32, ctypes.c_int, _vp]
+        S.rh_layer_shim.restype = ctypes.c_int
+        S.rh_fallthrough.argtypes = [ctypes.c_int]
+        S.rh_fallthrough.restype = ctypes.c_int
+        S.rh_op_id.argtypes = [ctypes.c_char_p]
+        S.rh_op_id.restype = ctypes.c_int
+        S.rh_shim_release.argtypes = [_vp]
         _shim = S
     return _shim
 
@@ -296,6 +311,29 @@ def ref_attn(kc, vc, q, k, v, slots, pos, n, n_head, window=0):
     return dst.reshape(n, n_head * khd)
 
 
+def ref_attn_radix(radix, kc, vc, q, k, v, pos, n, n_head, window=0):
+    """cpu_graph_op(OP_ATTN) with plan->radix = `radix` (a KvRadixCache*
+    made by another library); op_attn reads its req.slots / req.len through
+    the reference's struct layout (cpu_op.c:988-993)."""
+    n_kv, cap, khd = kc.shape
+    dst = np.zeros(n * n_head * khd, dtype=np.float32)
+    rc = ref().rh_attn_radix(radix, np.ascontiguousarray(q, dtype=np.float32).reshape(-1),
+                             np.ascontiguousarray(k, dtype=np.float32).reshape(-1),
+                             np.ascontiguousarray(v, dtype=np.float32).reshape(-1), dst,
+                             kc.reshape(-1), vc.reshape(-1), cap, pos, n, n_head, n_kv,
+                             khd, window)
+    if rc:
+        raise ValueError("reference op_attn returned false")
+    return dst.reshape(n, n_head * khd)
+
+
+def ref_radix_layout():
+    """offsetof / sizeof of the reference's KvRadixCache and KvSlotMeta fields."""
+    o = np.zeros(16, dtype=np.uint64)
+    ref().rh_radix_layout(o)
+    return [int(x) for x in o]
+
+
 def ref_rope(x, heads, hdim, rdim, pos, theta, neox):
     x = np.ascontiguousarray(x, dtype=np.float32)
     rows, od = x.shape
@@ -336,6 +374,10 @@ class RefKv:
     def append(self, tokens, pos, n):
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         return bool(self.R.rh_kv_append(self.h, t, pos, n))
+
+    def lookup_len(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        return int(self.R.rh_kv_lookup(self.h, t, t.size))
 
     def req(self):
         o = np.zeros(4, dtype=np.uint32)

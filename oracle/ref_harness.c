@@ -5,8 +5,11 @@
  * product's host kvcache, never linked into the product.
  *
  *   rh_attn      -> cpu_graph_op(OP_ATTN)      src/backend/cpu/cpu_op.c:1070,964
+ *   rh_attn_radix   the same over a prefix cache made by another library
+ *   rh_radix_layout offsets of the reference's KvRadixCache (kvcache.h:50-57)
  *   rh_rope      -> cpu_graph_op(OP_ROPE_*)    src/backend/cpu/cpu_op.c:653,674
  *   rh_kv_*      -> kv_cache_create/match/append/destroy  src/kvcache.c:122-270
+ *                   (rh_kv_lookup: a read-only raxFind walk over the same tree)
  *   rh_kvs_*     -> the same with a Session whose Graph registers one host
  *                   recurrent-state buffer (graph_state_bytes/save/load,
  *                   src/graph.c:360-408), and kv_cache_checkpoint/restore
@@ -17,6 +20,7 @@
  * op_attn reads are populated (cpu_op.c:968-993).
  */
 #include <math.h>
+#include <stddef.h>
 #include <stdlib.h>
 #include <string.h>
 #include "def.h"
@@ -28,9 +32,51 @@
 
 /* kc/vc: f32 [n_kv][cap][khd] (the reference layout, graph.c:852-858).
  * slots == NULL -> no radix (contiguous path, cpu_op.c:1034-1041). */
+static int attn_with(void *radix_ext, const float *q, const float *k, const float *v,
+                     float *dst, float *kc, float *vc, u32 cap, u32 *slots, u32 pos,
+                     u32 n, u32 n_head, u32 n_kv, u32 hd, u32 khd, u32 win);
+
 int rh_attn(const float *q, const float *k, const float *v, float *dst,
             float *kc, float *vc, u32 cap, u32 *slots, u32 pos, u32 n,
             u32 n_head, u32 n_kv, u32 hd, u32 khd, u32 win) {
+    return attn_with(NULL, q, k, v, dst, kc, vc, cap, slots, pos, n, n_head, n_kv, hd,
+                     khd, win);
+}
+
+/* The same OP_ATTN with plan->radix = `radix`, a prefix cache made elsewhere
+ * (libtlkv's kv_cache_create): op_attn reads its req.slots / req.len through
+ * the reference's struct layout (cpu_op.c:988-993). */
+int rh_attn_radix(void *radix, const float *q, const float *k, const float *v,
+                  float *dst, float *kc, float *vc, u32 cap, u32 pos, u32 n,
+                  u32 n_head, u32 n_kv, u32 hd, u32 win) {
+    if (!radix) return -1;
+    return attn_with(radix, q, k, v, dst, kc, vc, cap, NULL, pos, n, n_head, n_kv, hd, hd,
+                     win);
+}
+
+/* offsetof / sizeof of the reference's KvRadixCache fields (kvcache.h:50-57) */
+void rh_radix_layout(u64 *out) {
+    out[0] = offsetof(KvRadixCache, tree);
+    out[1] = offsetof(KvRadixCache, pool);
+    out[2] = offsetof(KvRadixCache, pool.n_free);
+    out[3] = offsetof(KvRadixCache, pool.free_stack);
+    out[4] = offsetof(KvRadixCache, meta);
+    out[5] = offsetof(KvRadixCache, req);
+    out[6] = offsetof(KvRadixCache, req.len);
+    out[7] = offsetof(KvRadixCache, req.shared_len);
+    out[8] = offsetof(KvRadixCache, req.active);
+    out[9] = offsetof(KvRadixCache, kv);
+    out[10] = offsetof(KvRadixCache, n_layer);
+    out[11] = offsetof(KvRadixCache, ctx_size);
+    out[12] = offsetof(KvRadixCache, enabled);
+    out[13] = sizeof(KvSlotMeta);
+    out[14] = offsetof(KvSlotMeta, last_used);
+    out[15] = offsetof(KvSlotMeta, in_tree);
+}
+
+static int attn_with(void *radix_ext, const float *q, const float *k, const float *v,
+                     float *dst, float *kc, float *vc, u32 cap, u32 *slots, u32 pos,
+                     u32 n, u32 n_head, u32 n_kv, u32 hd, u32 khd, u32 win) {
     ArchConfig cfg;
     memset(&cfg, 0, sizeof(cfg));
     cfg.n_head = n_head;
@@ -55,7 +101,7 @@ int rh_attn(const float *q, const float *k, const float *v, float *dst,
     GraphPlan plan;
     memset(&plan, 0, sizeof(plan));
     plan.cache = &kcache;
-    plan.radix = slots ? (void *)&radix : NULL;
+    plan.radix = radix_ext ? radix_ext : slots ? (void *)&radix : NULL;
 
     Graph g;
     memset(&g, 0, sizeof(g));
@@ -156,6 +202,22 @@ u32 rh_kv_match(void *p, const u32 *tokens, u32 n) {
 
 int rh_kv_append(void *p, const u32 *tokens, u32 pos, u32 n) {
     return kv_cache_append(((RhKv *)p)->c, tokens, pos, n) ? 1 : 0;
+}
+
+/* Longest cached prefix of tokens[0..n), read-only: the same raxFind walk
+ * kv_cache_match makes (kvcache.c:199-207: raw u32 keys of growing length,
+ * an in-tree slot behind each), without its reference counts, LRU touches or
+ * statistics. */
+u32 rh_kv_lookup(void *p, const u32 *tokens, u32 n) {
+    KvRadixCache *c = ((RhKv *)p)->c;
+    u32 i = 0;
+    for (; i < n; i++) {
+        void *v = raxFind(c->tree, (unsigned char *)tokens, (size_t)(i + 1) * sizeof(u32));
+        if (v == raxNotFound) break;
+        u32 slot = (u32)((uintptr_t)v - 1);
+        if (slot >= c->pool.n_slots || !c->meta[slot].in_tree) break;
+    }
+    return i;
 }
 
 /* req.len, req.shared_len, req.active, pool.n_free */

@@ -17,6 +17,7 @@
 #include "../../include/tl_kvcache.h"
 #include "tl_trie.h"
 
+#include <stddef.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -28,15 +29,22 @@ typedef struct {
     u32 slot;
 } HeapEnt;
 
+/* The fields up to `enabled` sit where the reference's struct puts them
+ * (src/kvcache.h:50-57), so code compiled against the reference's header —
+ * op_attn reading radix->req.slots / req.len (src/backend/cpu/cpu_op.c:988-993),
+ * the executor shim — reads this struct correctly.  TlKvRadixHead in
+ * tl_kvcache.h spells the layout; the asserts below hold the two together. */
 struct KvRadixCache {
-    TlTrie          trie;        /* token prefix -> slot + 1 */
+    TlTrie         *tree;        /* = &trie (the reference's `rax *tree` slot) */
     KvSlotPool      pool;
     KvSlotMeta     *meta;        /* [n_slots] */
     KvRequestState  req;
     KvCache        *kv;
-    Session        *s;
+    u32             n_layer;     /* 0: the KvCache is opaque to this library */
     u32             ctx_size;
     bool            enabled;
+    Session        *s;
+    TlTrie          trie;        /* token prefix -> slot + 1 */
     u32            *node_of;     /* [ctx_size] trie node holding each in-tree slot */
     /* cursor: trie node of the prefix cur_key[0..cur_len) */
     u32            *cur_key;     /* [ctx_size] */
@@ -56,6 +64,15 @@ struct KvRadixCache {
     KvRequstStats   stats;
     u32             dirty_lo;
 };
+
+_Static_assert(offsetof(struct KvRadixCache, tree) == offsetof(TlKvRadixHead, tree), "layout");
+_Static_assert(offsetof(struct KvRadixCache, pool) == offsetof(TlKvRadixHead, pool), "layout");
+_Static_assert(offsetof(struct KvRadixCache, meta) == offsetof(TlKvRadixHead, meta), "layout");
+_Static_assert(offsetof(struct KvRadixCache, req) == offsetof(TlKvRadixHead, req), "layout");
+_Static_assert(offsetof(struct KvRadixCache, kv) == offsetof(TlKvRadixHead, kv), "layout");
+_Static_assert(offsetof(struct KvRadixCache, n_layer) == offsetof(TlKvRadixHead, n_layer), "layout");
+_Static_assert(offsetof(struct KvRadixCache, ctx_size) == offsetof(TlKvRadixHead, ctx_size), "layout");
+_Static_assert(offsetof(struct KvRadixCache, enabled) == offsetof(TlKvRadixHead, enabled), "layout");
 
 /* ---- evictable-leaf heap --------------------------------------------------- */
 
@@ -251,6 +268,7 @@ KvRadixCache *kv_cache_create(Session *s, KvCache *kv, u32 ctx_size) {
     c->s = s;
     c->ctx_size = ctx_size;
     c->enabled = true;
+    c->tree = &c->trie;
     c->pool.n_slots = ctx_size;
     c->pool.free_stack = (u32 *)malloc((size_t)ctx_size * sizeof(u32));
     c->meta = (KvSlotMeta *)calloc(ctx_size, sizeof(KvSlotMeta));
