@@ -70,7 +70,9 @@ int  tl_session_execute(tl_session *s, const uint32_t *tokens, uint32_t n_tokens
  * then one slot upload and the K/V write-through (the part of OP_ATTN at
  * src/backend/cpu/cpu_op.c:995-1008) of the whole batch for every layer.
  * For callers that fill or extend a cache whose attention outputs they do
- * not need. */
+ * not need.  If a chunk's slot allocation fails, the rows of the chunks
+ * before it are still written, the position ends after them, and TL_ERANGE
+ * is returned (the reference's chunk loop stops at the same chunk). */
 int  tl_session_append(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                        const float *const *k, const float *const *v, uint32_t kv_stride);
 
@@ -116,6 +118,24 @@ KvRadixCache      *tl_session_radix(tl_session *s);            /* NULL without r
 const tl_kv_layer *tl_session_layer(const tl_session *s, uint32_t layer);   /* NULL if kv_q8 */
 const tl_kv_layer_q8 *tl_session_layer_q8(const tl_session *s, uint32_t layer); /* NULL if f16 */
 const uint32_t    *tl_session_device_slots(const tl_session *s);  /* device [ctx_size] */
+
+/* ---- device mirror of a prefix cache's request map, for executors that run
+ * OP_ATTN node by node (the reference's graph_execute, src/graph.c:1395-1413,
+ * calls kv_cache_append per chunk and then graph_compute; op_attn reads
+ * radix->req.slots, src/backend/cpu/cpu_op.c:988-993).  No reference
+ * counterpart: the reference's device backend has no slot table.
+ *
+ * tl_slot_mirror_sync uploads the part of req.slots[0, req.len) that changed
+ * since the previous sync of the same cache (all of it for a cache the mirror
+ * has not seen), in `stream` order, and returns the device table in
+ * *d_slots.  It consumes the cache's change mark (tl_kv_cache_take_dirty), so
+ * one cache feeds one mirror.  Fails with TL_ERANGE for a slot outside the
+ * mirror's ctx_size. */
+typedef struct tl_slot_mirror tl_slot_mirror;
+int  tl_slot_mirror_create(uint32_t ctx_size, tl_slot_mirror **out);
+void tl_slot_mirror_destroy(tl_slot_mirror *m);
+int  tl_slot_mirror_sync(tl_slot_mirror *m, KvRadixCache *radix, void *stream,
+                         const uint32_t **d_slots);
 
 #ifdef __cplusplus
 }

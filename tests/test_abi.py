@@ -105,7 +105,8 @@ def test_size_limits_and_empty_batches_need_no_device():
 @pytest.mark.skipif(not O.shim_available(), reason="executor shim not built (no reference tree)")
 def test_executor_shim_loads():
     S = O.shim()
-    for name in ("hip_graph_op", "hip_graph_op_set_slots", "hip_graph_op_set_stream"):
+    for name in ("hip_graph_op", "hip_graph_op_set_stream", "hip_graph_op_release",
+                 "hip_graph_op_fused_count"):
         assert hasattr(S, name)
 
 

@@ -30,6 +30,7 @@ struct tl_session {
     uint32_t       stage_pos;
     float          scale;
     int            has_ring;    /* some layer keeps only a window of rows */
+    uint32_t       min_ring;    /* smallest ring of those layers (0: none) */
     tl_state_seg  *state;       /* registered recurrent-state buffers (device) */
     uint32_t       n_state;
     size_t         state_bytes; /* their total (graph_state_bytes) */
@@ -79,7 +80,10 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
     for (uint32_t l = 0; l < cfg->n_layer; l++) {
         s->window[l] = cfg->window ? cfg->window[l] : 0;
         uint32_t ring = cfg->ring ? cfg->ring[l] : 0;
-        if (ring) s->has_ring = 1;
+        if (ring) {
+            s->has_ring = 1;
+            if (!s->min_ring || ring < s->min_ring) s->min_ring = ring;
+        }
         if (ring && (!s->window[l] || ring < s->window[l] + cfg->n_ubatch - 1)) {
             tl_session_destroy(s);
             return fail(TL_EINVAL, "session: a ring needs window + n_ubatch - 1 rows");
@@ -118,28 +122,34 @@ int tl_session_create(const tl_session_cfg *cfg, tl_session **out) {
     return TL_OK;
 }
 
-/* copy host words to device memory in stream order through the pinned ring */
-static int upload_words(tl_session *s, uint32_t *d_dst, const uint32_t *src, uint32_t n_words) {
-    hipStream_t st = (hipStream_t)s->cfg.stream;
+/* copy host words to device memory in stream order through a pinned ring of
+ * STAGE_WORDS words (*pos = next free word) */
+static int stage_upload(uint32_t *stage, uint32_t *pos, hipStream_t st, uint32_t *d_dst,
+                        const uint32_t *src, uint32_t n_words) {
     while (n_words) {
         uint32_t n = n_words;
         if (n > STAGE_WORDS) n = STAGE_WORDS;
-        if (s->stage_pos + n > STAGE_WORDS) {
+        if (*pos + n > STAGE_WORDS) {
             /* staged words may still be read by queued copies */
-            if (hipStreamSynchronize(st) != hipSuccess) return fail(TL_EHIP, "session: sync");
-            s->stage_pos = 0;
+            if (hipStreamSynchronize(st) != hipSuccess) return fail(TL_EHIP, "upload: sync");
+            *pos = 0;
         }
-        uint32_t *stg = s->stage + s->stage_pos;
+        uint32_t *stg = stage + *pos;
         memcpy(stg, src, (size_t)n * sizeof(uint32_t));
         if (hipMemcpyAsync(d_dst, stg, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice,
                            st) != hipSuccess)
-            return fail(TL_EHIP, "session: upload");
-        s->stage_pos += n;
+            return fail(TL_EHIP, "upload: copy");
+        *pos += n;
         d_dst += n;
         src += n;
         n_words -= n;
     }
     return TL_OK;
+}
+
+static int upload_words(tl_session *s, uint32_t *d_dst, const uint32_t *src, uint32_t n_words) {
+    return stage_upload(s->stage, &s->stage_pos, (hipStream_t)s->cfg.stream, d_dst, src,
+                        n_words);
 }
 
 /* upload req.slots[lo..hi) to the device mirror */
@@ -199,45 +209,75 @@ int tl_session_kv_prepare(tl_session *s, const uint32_t *tokens, uint32_t n,
     return TL_OK;
 }
 
+/* write-through of rows [pos, pos + n) of every layer: launches cover up to 64
+ * layers (the library splits them per 16), and on sessions with ring layers
+ * no launch spans more rows than the smallest ring, so positions p and p + R
+ * never land on one physical row within a launch (stream order then keeps
+ * the later row) */
+static int write_rows(tl_session *s, const float *const *k, const float *const *v,
+                      uint32_t kv_stride, uint32_t pos, uint32_t n) {
+    const uint32_t *sl = s->radix ? s->d_slots : NULL;
+    const uint32_t piece = s->min_ring ? s->min_ring : n;
+    for (uint32_t r0 = 0; r0 < n; r0 += piece) {
+        const uint32_t nr = n - r0 < piece ? n - r0 : piece;
+        for (uint32_t l0 = 0; l0 < s->cfg.n_layer; l0 += 64) {
+            const uint32_t nl = s->cfg.n_layer - l0 < 64 ? s->cfg.n_layer - l0 : 64;
+            const float *kk[64], *vv[64];
+            for (uint32_t j = 0; j < nl; j++) {
+                kk[j] = k[l0 + j] + (size_t)r0 * kv_stride;
+                vv[j] = v[l0 + j] + (size_t)r0 * kv_stride;
+            }
+            int rc = s->layers8
+                         ? tl_kv_append_layers_q8(&s->layers8[l0], nl, kk, vv, kv_stride, sl,
+                                                  pos + r0, nr, s->cfg.stream)
+                         : tl_kv_append_layers(&s->layers[l0], nl, kk, vv, kv_stride, sl,
+                                               pos + r0, nr, s->cfg.stream);
+            if (rc) return rc;
+        }
+    }
+    return TL_OK;
+}
+
 /* K/V write-through only (no attention): the prefix cache takes every
  * n_ubatch chunk of the batch first -- the same kv_cache_append calls, in the
  * same order, as the chunk loop below makes -- then one slot-table upload and
- * one write-through launch per 16 layers cover the whole batch.  No chunk's
- * rows can be evicted by a later chunk: the request pins its slots. */
+ * the write-through of the whole batch (write_rows).  No chunk's rows can be
+ * evicted by a later chunk: the request pins its slots.  If a chunk's slot
+ * allocation fails, the rows of the chunks before it are still written (as
+ * the reference's chunk loop would have written them) and the session
+ * position ends after them. */
 static int append_only(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
                        const float *const *k, const float *const *v, uint32_t kv_stride) {
     const uint32_t pos = s->n_tokens;
     if ((uint64_t)pos + n_tokens > s->cfg.ctx_size)
         return fail(TL_ERANGE, "append: batch exceeds ctx_size");
     memcpy(s->tokens + pos, tokens, (size_t)n_tokens * sizeof(uint32_t));
+    uint32_t done = n_tokens;
+    int err = TL_OK;
     if (s->radix) {
-        for (uint32_t done = 0; done < n_tokens;) {
+        for (done = 0; done < n_tokens;) {
             uint32_t chunk = n_tokens - done;
             if (chunk > s->cfg.n_ubatch) chunk = s->cfg.n_ubatch;
-            if (!kv_cache_append(s->radix, s->tokens, pos + done, chunk))
-                return fail(TL_ERANGE, "KV slot allocation failed");
+            if (!kv_cache_append(s->radix, s->tokens, pos + done, chunk)) {
+                err = TL_ERANGE;
+                break;
+            }
             done += chunk;
         }
         const KvRequestState *req = tl_kv_cache_req(s->radix);
-        if (req->len < pos + n_tokens) return fail(TL_ERANGE, "append: request map too short");
+        if (req->len < pos + done) return fail(TL_ERANGE, "append: request map too short");
         uint32_t lo = tl_kv_cache_take_dirty(s->radix);
-        if (lo != KV_SLOT_NONE && lo < pos + n_tokens) {
-            int rc = upload_slots(s, lo, pos + n_tokens);
+        if (lo != KV_SLOT_NONE && lo < pos + done) {
+            int rc = upload_slots(s, lo, pos + done);
             if (rc) return rc;
         }
     }
-    const uint32_t *sl = s->radix ? s->d_slots : NULL;
-    for (uint32_t l0 = 0; l0 < s->cfg.n_layer; l0 += 64) {
-        const uint32_t nl = s->cfg.n_layer - l0 < 64 ? s->cfg.n_layer - l0 : 64;
-        int rc = s->layers8
-                     ? tl_kv_append_layers_q8(&s->layers8[l0], nl, k + l0, v + l0, kv_stride, sl,
-                                              pos, n_tokens, s->cfg.stream)
-                     : tl_kv_append_layers(&s->layers[l0], nl, k + l0, v + l0, kv_stride, sl,
-                                           pos, n_tokens, s->cfg.stream);
+    if (done) {
+        int rc = write_rows(s, k, v, kv_stride, pos, done);
         if (rc) return rc;
     }
-    s->n_tokens = pos + n_tokens;
-    return TL_OK;
+    s->n_tokens = pos + done;
+    return err ? fail(err, "KV slot allocation failed") : TL_OK;
 }
 
 /* The chunk loop of graph_execute (src/graph.c:1395-1413). */
@@ -465,3 +505,68 @@ const tl_kv_layer *tl_session_layer(const tl_session *s, uint32_t layer) {
     return (s && s->layers && layer < s->cfg.n_layer) ? &s->layers[layer] : NULL;
 }
 const uint32_t *tl_session_device_slots(const tl_session *s) { return s ? s->d_slots : NULL; }
+
+/* ---- slot mirror ---------------------------------------------------------- */
+
+struct tl_slot_mirror {
+    uint32_t      ctx_size;
+    uint32_t     *d_slots;     /* device [ctx_size] */
+    uint32_t     *stage;       /* pinned [STAGE_WORDS] */
+    uint32_t      stage_pos;
+    KvRadixCache *seen;        /* the cache whose change marks the mirror follows */
+};
+
+int tl_slot_mirror_create(uint32_t ctx_size, tl_slot_mirror **out) {
+    if (!out || ctx_size == 0) return fail(TL_EINVAL, "slot mirror: bad arguments");
+    *out = NULL;
+    tl_slot_mirror *m = (tl_slot_mirror *)calloc(1, sizeof(*m));
+    if (!m) return fail(TL_ENOMEM, "slot mirror: host allocation");
+    m->ctx_size = ctx_size;
+    if (hipMalloc((void **)&m->d_slots, (size_t)ctx_size * sizeof(uint32_t)) != hipSuccess ||
+        hipHostMalloc((void **)&m->stage, STAGE_WORDS * sizeof(uint32_t), 0) != hipSuccess) {
+        m->stage = NULL;
+        tl_slot_mirror_destroy(m);
+        return fail(TL_ENOMEM, "slot mirror: allocation");
+    }
+    *out = m;
+    return TL_OK;
+}
+
+void tl_slot_mirror_destroy(tl_slot_mirror *m) {
+    if (!m) return;
+    if (m->d_slots) (void)hipFree(m->d_slots);
+    if (m->stage) (void)hipHostFree(m->stage);
+    free(m);
+}
+
+int tl_slot_mirror_sync(tl_slot_mirror *m, KvRadixCache *radix, void *stream,
+                        const uint32_t **d_slots) {
+    if (d_slots) *d_slots = NULL;
+    if (!m || !radix) return fail(TL_EINVAL, "slot mirror: missing mirror or cache");
+    const KvRequestState *req = tl_kv_cache_req(radix);
+    uint32_t lo = tl_kv_cache_take_dirty(radix);
+    if (m->seen != radix) {
+        lo = 0;   /* a cache this mirror has not followed: upload the whole map */
+        m->seen = radix;
+    }
+    const uint32_t len = req->len;
+    if (len > m->ctx_size) {
+        m->seen = NULL;
+        return fail(TL_ERANGE, "slot mirror: request longer than the mirror");
+    }
+    if (lo != KV_SLOT_NONE && lo < len) {
+        for (uint32_t i = lo; i < len; i++)
+            if (req->slots[i] >= m->ctx_size) {
+                m->seen = NULL;   /* re-upload everything next time */
+                return fail(TL_ERANGE, "slot mirror: slot outside the cache");
+            }
+        int rc = stage_upload(m->stage, &m->stage_pos, (hipStream_t)stream, m->d_slots + lo,
+                              req->slots + lo, len - lo);
+        if (rc) {
+            m->seen = NULL;
+            return rc;
+        }
+    }
+    if (d_slots) *d_slots = m->d_slots;
+    return TL_OK;
+}
