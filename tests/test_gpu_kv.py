@@ -511,3 +511,133 @@ def test_attn_rejects_bad_arguments_without_side_effects(T):
     assert lib.tl_attn(R.desc, a, None) == TL_EINVAL   # window + n - 1 > ring
     sync(T)
     assert bool((out == 7.0).all())
+
+
+# ---- depth, RoPE sweep, full-size batches, concurrent streams ---------------
+
+@pytest.mark.parametrize("splits", [0, 1, 5])
+def test_prefill_deep_chunk_vs_oracle(T, splits):
+    """Config 4's last chunk depth: 64 query rows at pos 32256 over 32320 keys
+    (505 key tiles) through a permuted slot table, heads reduced to 8 / 2 so
+    the oracle stays fast; automatic key splits and forced 1 and 5 splits
+    (the merge kernel)."""
+    import tlkv
+    n_head, n_kv, hd, pos, n = 8, 2, 128, 32256, 64
+    cap = pos + n + 64
+    rng = np.random.default_rng(32256 + splits)
+    slots = rng.permutation(cap).astype(np.uint32)
+    with tlkv.tuning(tlkv.TUNE_PREFILL_SPLITS, splits):
+        out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, 0, slots, seed=77)
+    assert np.abs(out - o16).max() < TOL
+    assert np.abs(out - o32).max() < TOL
+
+
+ROPE_SWEEP = [
+    # neox, theta, heads, head_dim, rope_dim: the configs' rotations
+    (0, 5e5, 8, 128, 128),    # configs 1 / 4 (Llama NORM)
+    (0, 5e5, 8, 64, 64),
+    (1, 1e6, 4, 128, 128),    # configs 2 / 3 (Qwen NEOX), config 5 global
+    (1, 1e4, 4, 256, 256),    # config 5 local
+    (1, 1e6, 4, 256, 64),     # partial rotation
+]
+
+
+@pytest.mark.parametrize("pos", [0, 8192, 16384, 33791])
+@pytest.mark.parametrize("rp", ROPE_SWEEP)
+def test_rope_sweep_vs_oracle_and_reference(T, rp, pos):
+    """tl_rope at the configs' theta / NORM-NEOX / rope_dim and positions up to
+    config 4's last.  The angle pos * theta_i is formed in f32 on every side;
+    theta_i = 1 / powf(base, e) may differ by an ulp between libms, which moves
+    the angle by up to pos * theta_i * 2^-23: the tolerance scales with pos."""
+    import tlkv
+    neox, theta, heads, hd, rdim = rp
+    rng = np.random.default_rng(pos + hd + rdim)
+    rows_n = 16
+    x = rng.standard_normal((rows_n, heads * hd)).astype(np.float32)
+    dx = dev(T, x)
+    tlkv.check(tlkv.lib().tl_rope(tlkv.ptr(dx), rows_n, heads * hd, heads, hd, rdim, pos,
+                                  theta, neox, None))
+    sync(T)
+    got = host(dx)
+    tol = 2e-6 + float(np.abs(x).max()) * (pos + rows_n) * 2.4e-7
+    assert np.abs(got - O.rope(x, heads, hd, rdim, pos, theta, neox)).max() < tol
+    if O.ref_available():
+        assert np.abs(got - O.ref_rope(x, heads, hd, rdim, pos, theta, neox)).max() < tol
+    # dims past rope_dim are copied unchanged
+    if rdim < hd:
+        xs, gs = x.reshape(rows_n, heads, hd), got.reshape(rows_n, heads, hd)
+        assert np.array_equal(xs[..., rdim:], gs[..., rdim:])
+
+
+def test_decode_batch_sessions_full_size(T):
+    """Config 2 at full size: 8 sessions x 8193 visible keys (gqa 7, permuted
+    slot tables), one batched launch with the fused append, against the
+    oracle per session."""
+    import tlkv
+    n_head, n_kv, hd, n_seq, pos = 28, 4, 128, 8, 8192
+    cap = 8704
+    rng = np.random.default_rng(8192)
+    seqs, refs, keep = [], [], []
+    for s in range(n_seq):
+        slots = rng.permutation(cap).astype(np.uint32)
+        L = tlkv.Layer(cap, n_kv, hd)
+        hk, hv = rows(rng, pos, n_kv * hd), rows(rng, pos, n_kv * hd)
+        ds = dev(T, slots)
+        tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, hk)),
+                                           tlkv.ptr(dev(T, hv)), n_kv * hd,
+                                           tlkv.ptr(ds), 0, pos, None))
+        C = O.Cache(cap, n_kv, hd)
+        C.append(hk, hv, slots, 0, pos)
+        q, k, v = rows(rng, 1, n_head * hd), rows(rng, 1, n_kv * hd), rows(rng, 1, n_kv * hd)
+        dq, dk, dv = dev(T, q), dev(T, k), dev(T, v)
+        out = T.zeros((1, n_head * hd), dtype=T.float32, device="cuda")
+        keep += [L, ds, dq, dk, dv]
+        seqs.append(tlkv.DecodeSeq(L.desc, ds.data_ptr(), pos, 0, dq.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), out.data_ptr()))
+        refs.append((out, O.attn(C, q, k, v, slots, pos, 1, n_head)))
+    arr = (tlkv.DecodeSeq * n_seq)(*seqs)
+    tlkv.check(tlkv.lib().tl_attn_decode_batch(arr, n_seq, n_head, 0, O.scale_of(hd), None))
+    sync(T)
+    for i, (out, ref) in enumerate(refs):
+        assert np.abs(host(out) - ref).max() < TOL, f"session {i}"
+
+
+def test_two_streams_interleaved_decode(T):
+    """Two sessions on two streams (default priority) decode in turn without
+    synchronising between launches: each stream has its own split partials and
+    merge counters, so every output matches the oracle."""
+    import tlkv
+    n_head, n_kv, hd, pos0, steps = 32, 8, 128, 6000, 6
+    cap = pos0 + steps
+    streams = [T.cuda.Stream(), T.cuda.Stream()]
+    sess = []
+    for i in range(2):
+        rng = np.random.default_rng(900 + i)
+        slots = rng.permutation(cap).astype(np.uint32)
+        L = tlkv.Layer(cap, n_kv, hd)
+        hk, hv = rows(rng, pos0, n_kv * hd), rows(rng, pos0, n_kv * hd)
+        ds = dev(T, slots)
+        tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, hk)),
+                                           tlkv.ptr(dev(T, hv)), n_kv * hd, tlkv.ptr(ds),
+                                           0, pos0, None))
+        C = O.Cache(cap, n_kv, hd)
+        C.append(hk, hv, slots, 0, pos0)
+        qs = [rows(rng, 1, n_head * hd) for _ in range(steps)]
+        ks = [rows(rng, 1, n_kv * hd) for _ in range(steps)]
+        vs = [rows(rng, 1, n_kv * hd) for _ in range(steps)]
+        outs = [T.zeros((1, n_head * hd), dtype=T.float32, device="cuda") for _ in range(steps)]
+        sess.append(dict(L=L, ds=ds, C=C, slots=slots, q=qs, k=ks, v=vs, out=outs,
+                         dq=[dev(T, x) for x in qs], dk=[dev(T, x) for x in ks],
+                         dv=[dev(T, x) for x in vs]))
+    T.cuda.synchronize()
+    for t in range(steps):
+        for i, S in enumerate(sess):
+            a = tlkv.attn_args(S["dq"][t], S["dk"][t], S["dv"][t], S["out"][t], S["ds"],
+                               pos0 + t, 1, n_head, hd, n_kv, 0, O.scale_of(hd))
+            tlkv.check(tlkv.lib().tl_attn(S["L"].desc, a, streams[i].cuda_stream))
+    sync(T)
+    for i, S in enumerate(sess):
+        for t in range(steps):
+            ref = O.attn(S["C"], S["q"][t], S["k"][t], S["v"][t], S["slots"], pos0 + t, 1,
+                         n_head)
+            assert np.abs(host(S["out"][t]) - ref).max() < TOL, f"session {i} step {t}"

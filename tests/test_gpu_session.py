@@ -280,3 +280,67 @@ def test_session_append_only_multi_chunk(T, kv_q8):
     assert (st.hit_tokens, st.evictions, st.allocations) == (
         ref.stats()["hit_tokens"], ref.stats()["evictions"], ref.stats()["allocations"])
     assert st.evictions > 0
+
+
+@pytest.mark.parametrize("kv_q8", [False, True])
+def test_session_append_only_ring_layer(T, kv_q8):
+    """tl_session_append with a batch longer than a ring layer's ring: the ring
+    keeps the last `ring` positions, each at row p % ring, bit for bit (no
+    launch may carry positions p and p + ring together), and the global layer
+    holds every row behind the slot map."""
+    import tlkv
+    n_layer, nkv, hd, ctx, ub, win = 2, 2, 64, 160, 8, 16
+    ring = win + ub - 1
+    kd = nkv * hd
+    S = tlkv.Session(n_layer, 8, nkv, hd, ctx, ub, window=[win, 0], ring=[ring, 0],
+                     kv_q8=kv_q8)
+    rng = np.random.default_rng(41)
+    toks = [int(x) for x in rng.integers(0, 1000, size=150)]
+    arr = np.array(toks, np.uint32)
+    S.kv_prepare(arr)
+    allk = [np.stack([prefix_rows(toks, p, kd, b"k%d" % l) for p in range(len(toks))])
+            for l in range(n_layer)]
+    allv = [np.stack([prefix_rows(toks, p, kd, b"v%d" % l) for p in range(len(toks))])
+            for l in range(n_layer)]
+    # two batches: 97 rows (over four rings' worth), then 53
+    for a, b in ((0, 97), (97, 150)):
+        S.append(arr[a:b], [T.from_numpy(x[a:b].copy()).cuda() for x in allk],
+                 [T.from_numpy(x[a:b].copy()).cuda() for x in allv], kd)
+        T.cuda.synchronize()
+        n = b
+        last = np.arange(n - ring, n)
+        for l, sl in ((0, (last % ring).astype(np.int32)),
+                      (1, S.radix_slots(n).astype(np.int32))):
+            pos = last if l == 0 else np.arange(n)
+            dsl = T.from_numpy(sl).cuda()
+            m = len(sl)
+            if kv_q8:
+                src = S.layer_q8(l)
+                phys = tlkv.KvLayerQ8(src.k, src.v, src.ks, src.vs,
+                                      ring if l == 0 else src.cap, nkv, hd, 0)
+                ko = T.zeros((m, nkv, hd), dtype=T.int8, device="cuda")
+                kso = T.zeros((m, nkv, hd // 32), dtype=T.int16, device="cuda")
+                vo, vso = T.zeros_like(ko), T.zeros_like(kso)
+                tlkv.check(tlkv.lib().tl_kv_gather_q8(phys, tlkv.ptr(dsl), m,
+                                                      tlkv.ptr(ko), tlkv.ptr(kso), tlkv.ptr(vo),
+                                                      tlkv.ptr(vso), None))
+                T.cuda.synchronize()
+                qk, dk = O.q8_quantize(allk[l][pos].reshape(m, nkv, hd))
+                qv, dv = O.q8_quantize(allv[l][pos].reshape(m, nkv, hd))
+                assert np.array_equal(ko.cpu().numpy(), qk), f"layer {l} rows {n}"
+                assert np.array_equal(kso.cpu().numpy().view(np.uint16), dk)
+                assert np.array_equal(vo.cpu().numpy(), qv)
+                assert np.array_equal(vso.cpu().numpy().view(np.uint16), dv)
+            else:
+                src = S.layer(l)
+                phys = tlkv.KvLayer(src.k, src.v, ring if l == 0 else src.cap, nkv, hd, 0)
+                ko = T.zeros((m, nkv, hd), dtype=T.float16, device="cuda")
+                vo = T.zeros_like(ko)
+                tlkv.check(tlkv.lib().tl_kv_gather(phys, tlkv.ptr(dsl), m,
+                                                   tlkv.ptr(ko), tlkv.ptr(vo), None))
+                T.cuda.synchronize()
+                assert np.array_equal(ko.cpu().numpy().view(np.uint16).reshape(m, -1),
+                                      O.f16_bits(allk[l][pos])), f"layer {l} rows {n}"
+                assert np.array_equal(vo.cpu().numpy().view(np.uint16).reshape(m, -1),
+                                      O.f16_bits(allv[l][pos]))
+

@@ -138,7 +138,7 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     if (n_split > 1) {
         TlWorkspace *w;
         size_t parts = (size_t)n_rows_total * p.n_head * n_split;
-        int rc = tl_workspace_get(parts * head_dim, parts, in_kernel_merge ? n_groups : 0, &w);
+        int rc = tl_workspace_get(st, parts * head_dim, parts, in_kernel_merge ? n_groups : 0, &w);
         if (rc) return rc;
         p.ws_acc = w->acc;
         p.ws_ml = (float2 *)w->ml;

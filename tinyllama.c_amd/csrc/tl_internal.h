@@ -107,7 +107,19 @@ uint32_t tl_tune(int key);
 
 /* Most keys one decode workgroup handles (its slot indices are staged in LDS). */
 #define TL_DEC_MAX_CHUNK 2048
-int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters, TlWorkspace **out);
+/* split partials for a launch on `st`: the stream's own workspace (grown on
+ * demand), or inside a TlWsFixed scope the fixed region (TL_ERANGE when it
+ * is too small; nothing is allocated) */
+int tl_workspace_get(hipStream_t st, size_t acc_floats, size_t ml_pairs, size_t counters,
+                     TlWorkspace **out);
+/* Scope in which this thread's launches take their partials from `w`. */
+struct TlWsFixed {
+    explicit TlWsFixed(TlWorkspace *w);
+    ~TlWsFixed();
+    TlWorkspace *prev;
+};
+/* partial floats of the fixed region in scope, 0 outside one */
+size_t tl_workspace_fixed_acc(void);
 int tl_launch_append(const AppendParams &p, uint32_t n_seg, hipStream_t stream);
 /* q8: the seq[] rows are a Q8_0 cache (no fused append: kin must be NULL) */
 int tl_launch_decode(DecParams &p, uint32_t n_rows_total, uint32_t head_dim, uint32_t G,

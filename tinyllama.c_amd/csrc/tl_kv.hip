@@ -44,21 +44,44 @@ extern "C" const char *tl_last_error(void) { return g_err; }
 
 
 /* ------------------------------------------------------------------------ */
-/* per-device workspace for split-K partials                                 */
+/* split-K workspace, one per (device, stream)                               */
 /* ------------------------------------------------------------------------ */
 
+/* Each stream that launches split attention gets its own partials and merge
+ * counters, so launches queued on different streams (two sessions, each on
+ * its own stream) never share them; launches on one stream run in order.
+ * The table holds TL_WS_STREAMS streams per device; a further stream takes
+ * the least recently used entry (its buffers are freed, which waits for the
+ * device). */
 #define TL_MAX_DEV 16
-static TlWorkspace g_ws[TL_MAX_DEV];
+#define TL_WS_STREAMS 16
+struct WsSlot {
+    hipStream_t st;
+    bool live;
+    u64 used;
+    TlWorkspace w;
+};
+static WsSlot g_ws[TL_MAX_DEV][TL_WS_STREAMS];
+static u64 g_ws_clock;
+static std::mutex g_ws_mu;
+static thread_local TlWorkspace *g_ws_fixed;   /* set by TlWsFixed */
 
-int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters,
-                     TlWorkspace **out) {
-    int dev = 0;
-    HIP_TRY(hipGetDevice(&dev));
-    if (dev < 0 || dev >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", dev);
-    TlWorkspace *w = &g_ws[dev];
+TlWsFixed::TlWsFixed(TlWorkspace *w) : prev(g_ws_fixed) { g_ws_fixed = w; }
+TlWsFixed::~TlWsFixed() { g_ws_fixed = prev; }
+size_t tl_workspace_fixed_acc(void) { return g_ws_fixed ? g_ws_fixed->acc_cap : 0; }
+
+static void ws_release(TlWorkspace *w) {
+    if (w->acc) (void)hipFree(w->acc);
+    if (w->ml) (void)hipFree(w->ml);
+    if (w->cnt) (void)hipFree(w->cnt);
+    memset(w, 0, sizeof(*w));
+}
+
+static int ws_grow(TlWorkspace *w, size_t acc_floats, size_t ml_pairs, size_t counters) {
     if (acc_floats > w->acc_cap) {
         if (w->acc) HIP_TRY(hipFree(w->acc));
         w->acc = NULL;
+        w->acc_cap = 0;
         size_t cap = acc_floats + acc_floats / 4 + 1024;
         if (hipMalloc((void **)&w->acc, cap * sizeof(float)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu floats", cap);
@@ -67,6 +90,7 @@ int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters,
     if (ml_pairs > w->ml_cap) {
         if (w->ml) HIP_TRY(hipFree(w->ml));
         w->ml = NULL;
+        w->ml_cap = 0;
         size_t cap = ml_pairs + ml_pairs / 4 + 256;
         if (hipMalloc((void **)&w->ml, cap * sizeof(float2)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu pairs", cap);
@@ -75,6 +99,7 @@ int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters,
     if (counters > w->cnt_cap) {
         if (w->cnt) HIP_TRY(hipFree(w->cnt));
         w->cnt = NULL;
+        w->cnt_cap = 0;
         size_t cap = counters + 256;
         if (hipMalloc((void **)&w->cnt, cap * sizeof(u32)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu counters", cap);
@@ -83,14 +108,48 @@ int tl_workspace_get(size_t acc_floats, size_t ml_pairs, size_t counters,
         HIP_TRY(hipDeviceSynchronize());
         w->cnt_cap = cap;
     }
-    *out = w;
+    return TL_OK;
+}
+
+int tl_workspace_get(hipStream_t st, size_t acc_floats, size_t ml_pairs, size_t counters,
+                     TlWorkspace **out) {
+    if (g_ws_fixed) {
+        /* a no-allocation call: the caller's fixed region or nothing */
+        TlWorkspace *w = g_ws_fixed;
+        if (acc_floats > w->acc_cap || ml_pairs > w->ml_cap || counters > w->cnt_cap)
+            return tl_fail(TL_ERANGE,
+                           "scratch: %zu partial floats, %zu pairs, %zu counters exceed "
+                           "%zu / %zu / %zu",
+                           acc_floats, ml_pairs, counters, w->acc_cap, w->ml_cap, w->cnt_cap);
+        *out = w;
+        return TL_OK;
+    }
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", dev);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    WsSlot *tab = g_ws[dev], *hit = nullptr;
+    for (int i = 0; i < TL_WS_STREAMS && !hit; i++)
+        if (tab[i].live && tab[i].st == st) hit = &tab[i];
+    if (!hit) {
+        /* a free entry, else the least recently used one */
+        for (int i = 0; i < TL_WS_STREAMS; i++)
+            if (!hit || (hit->live && (!tab[i].live || tab[i].used < hit->used))) hit = &tab[i];
+        if (hit->live) ws_release(&hit->w);
+        hit->live = true;
+        hit->st = st;
+    }
+    hit->used = ++g_ws_clock;
+    int rc = ws_grow(&hit->w, acc_floats, ml_pairs, counters);
+    if (rc) return rc;
+    *out = &hit->w;
     return TL_OK;
 }
 
 extern "C" int tl_init(int device) {
     HIP_TRY(hipSetDevice(device));
     TlWorkspace *w;
-    return tl_workspace_get(1 << 20, 1 << 14, 4096, &w);
+    return tl_workspace_get(nullptr, 1 << 20, 1 << 14, 4096, &w);
 }
 
 /* launch-shape overrides: seeded once from the environment, then only

@@ -97,7 +97,7 @@ int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &
     if (ns > 1) {
         TlWorkspace *w;
         size_t parts = (size_t)a->n * a->n_head * ns;
-        int rc = tl_workspace_get(parts * D, parts, 0, &w);
+        int rc = tl_workspace_get(st, parts * D, parts, 0, &w);
         if (rc) return rc;
         p.ws_acc = w->acc;
         p.ws_ml = (float2 *)w->ml;
