@@ -187,6 +187,16 @@ int tl_kv_append_rope(const tl_kv_layer *L, const float *k, const float *v,
  * split-K LDS kernel, larger ones the MFMA chunked-prefill kernel. */
 int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
 
+/* tl_attn that allocates nothing.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops).  The split partials and merge counters live in one
+ * fixed region per GPU (32 MiB, held until the process ends; set up by
+ * tl_init or the first call on a device).  Calls needing more than it holds
+ * fail with TL_ERANGE (prefill batches take fewer key splits to fit).  All
+ * calls on one GPU share the region: calls that overlap on one GPU (two
+ * streams, two threads) race and must be serialised by the caller. */
+int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
+
 /* Attention only (no append): the rows at positions < pos+n are assumed
  * already in the cache. */
 int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, void *stream);

@@ -1,0 +1,79 @@
+"""tl_attn_noalloc (the entry point that allocates nothing: split partials and
+merge counters in the library's fixed per-GPU region) against tl_attn on the
+same inputs, through the C ABI: calls in a row, each followed by a smaller
+one, so the second reads a region the first left behind.  Decode outputs are
+bit-identical (same kernels, same split count); prefill batches may take
+fewer key splits to fit the region, so they agree within 1e-4 and both stay
+within 2e-3 of the oracle.  The appended cache rows are identical."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def T():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    import tlkv
+    tlkv.check(tlkv.lib().tl_init(0))
+    return torch
+
+
+def _pair(T, n_head, n_kv, hd, cap, pos, n, window, seed):
+    """Two layers with the same history; OP_ATTN of the same batch through
+    tl_attn and tl_attn_noalloc.  Returns (out_attn, out_noalloc, oracle,
+    layers)."""
+    import tlkv
+    rng = np.random.default_rng(seed)
+    kd = n_kv * hd
+    hk = rng.standard_normal((pos, kd)).astype(np.float32)
+    hv = rng.standard_normal((pos, kd)).astype(np.float32)
+    q = rng.standard_normal((n, n_head * hd)).astype(np.float32)
+    k = rng.standard_normal((n, kd)).astype(np.float32)
+    v = rng.standard_normal((n, kd)).astype(np.float32)
+    slots = rng.permutation(cap).astype(np.uint32)
+    ds = T.from_numpy(slots).cuda()
+    dhk, dhv = T.from_numpy(hk).cuda(), T.from_numpy(hv).cuda()
+    dq, dk, dv = (T.from_numpy(x).cuda() for x in (q, k, v))
+    outs, layers = [], []
+    for fn in ("tl_attn", "tl_attn_noalloc"):
+        L = tlkv.Layer(cap, n_kv, hd)
+        if pos:
+            tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dhk), tlkv.ptr(dhv), kd,
+                                               tlkv.ptr(ds), 0, pos, None))
+        out = T.full((n, n_head * hd), float("nan"), dtype=T.float32, device="cuda")
+        a = tlkv.attn_args(dq, dk, dv, out, ds, pos, n, n_head, hd, n_kv, window,
+                           O.scale_of(hd))
+        tlkv.check(getattr(tlkv.lib(), fn)(L.desc, a, None))
+        T.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+        layers.append(L)
+    C = O.Cache(cap, n_kv, hd)
+    C.append(hk, hv, slots, 0, pos)
+    ref = O.attn(C, q, k, v, slots, pos, n, n_head, window=window)
+    return outs[0], outs[1], ref, layers
+
+
+@pytest.mark.parametrize("kind", ["decode", "prefill"])
+def test_noalloc_equals_attn_twice(T, kind):
+    if kind == "decode":
+        # config 4's last step, then a smaller windowed multi-row decode
+        calls = [(32, 8, 128, 33800, 33791, 1, 0), (16, 2, 128, 4096, 3000, 5, 700)]
+    else:
+        # a config-4 chunk at depth, then a smaller gqa-7 chunk
+        calls = [(32, 8, 128, 8800, 8192, 512, 0), (28, 4, 128, 1200, 300, 100, 0)]
+    for i, (nh, nkv, hd, cap, pos, n, win) in enumerate(calls):
+        base, noalloc, ref, layers = _pair(T, nh, nkv, hd, cap, pos, n, win, seed=100 + i)
+        assert np.isfinite(noalloc).all()
+        if kind == "decode":
+            assert np.array_equal(base.view(np.uint32), noalloc.view(np.uint32)), f"call {i}"
+        else:
+            assert np.abs(base - noalloc).max() < 1e-4, f"call {i}"
+        assert np.abs(noalloc - ref).max() < TOL, f"call {i}"
+        k0 = layers[0].k.cpu().numpy().view(np.uint16)
+        k1 = layers[1].k.cpu().numpy().view(np.uint16)
+        assert np.array_equal(k0, k1), f"call {i}: appended rows differ"

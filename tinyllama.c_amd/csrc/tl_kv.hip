@@ -146,8 +146,50 @@ int tl_workspace_get(hipStream_t st, size_t acc_floats, size_t ml_pairs, size_t 
     return TL_OK;
 }
 
+/* ------------------------------------------------------------------------ */
+/* fixed scratch for the no-allocation entry point (tl_attn_noalloc)         */
+/* ------------------------------------------------------------------------ */
+
+/* One region per GPU for the whole process: split partials, (max, sum)
+ * pairs and merge counters of tl_attn_noalloc.  Host code never uses the
+ * symbol's name as an address: each device's copy sits at the address
+ * hipGetSymbolAddress returns with that device current (g_scratch_dev). */
+#define TL_SCRATCH_ACC_FLOATS (30u << 18)   /* 30 MiB of partials */
+#define TL_SCRATCH_ML_PAIRS (1u << 17)      /* 1 MiB of (max, sum) pairs */
+#define TL_SCRATCH_COUNTERS (1u << 18)      /* 1 MiB of merge counters */
+#define TL_SCRATCH_BYTES                                                      \
+    ((size_t)TL_SCRATCH_ACC_FLOATS * 4 + (size_t)TL_SCRATCH_ML_PAIRS * 8 +   \
+     (size_t)TL_SCRATCH_COUNTERS * 4)
+static __device__ __align__(256) unsigned char scratch[TL_SCRATCH_BYTES];
+static unsigned char *g_scratch_dev[TL_MAX_DEV];
+static std::mutex g_scratch_mu;
+
+/* the calling thread's device's scratch address, set up on first use (the
+ * counters zeroed once; every launch leaves them at zero) */
+static int scratch_setup(int dev, unsigned char **out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return tl_fail(TL_EHIP, "scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        unsigned char *base = (unsigned char *)ptr;
+        HIP_TRY(hipMemset(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4 +
+                              (size_t)TL_SCRATCH_ML_PAIRS * 8,
+                          0, (size_t)TL_SCRATCH_COUNTERS * 4));
+        HIP_TRY(hipDeviceSynchronize());
+        g_scratch_dev[dev] = base;
+    }
+    *out = g_scratch_dev[dev];
+    return TL_OK;
+}
+
 extern "C" int tl_init(int device) {
     HIP_TRY(hipSetDevice(device));
+    if (device < 0 || device >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", device);
+    unsigned char *sc;
+    int rc = scratch_setup(device, &sc);
+    if (rc) return rc;
     TlWorkspace *w;
     return tl_workspace_get(nullptr, 1 << 20, 1 << 14, 4096, &w);
 }
@@ -690,6 +732,42 @@ extern "C" int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, voi
     RopeCfg rc0;
     rope_cfg(L, nullptr, rc0);
     return attn_core(L, a, false, rc0, (hipStream_t)stream);
+}
+
+/* zero n words (the merge counters a launch will use) */
+__global__ __launch_bounds__(256) void zero_words_kernel(u32 *p, u32 n) {
+    for (u32 i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+extern "C" int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
+    int rc = check_args(L, a);
+    if (rc) return rc;
+    if (a->n == 0) return TL_OK;
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", dev);
+    unsigned char *base;
+    rc = scratch_setup(dev, &base);
+    if (rc) return rc;
+    TlWorkspace w;
+    w.acc = (float *)base;
+    w.ml = (float *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4);
+    w.cnt = (u32 *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4 + (size_t)TL_SCRATCH_ML_PAIRS * 8);
+    w.acc_cap = TL_SCRATCH_ACC_FLOATS;
+    w.ml_cap = TL_SCRATCH_ML_PAIRS;
+    w.cnt_cap = TL_SCRATCH_COUNTERS;
+    const u64 groups = (u64)a->n * L->n_kv_head;
+    if (groups > w.cnt_cap) return tl_fail(TL_ERANGE, "scratch: %llu row groups", (unsigned long long)groups);
+    /* the counters of this call start at zero whatever an earlier
+     * (overlapping) call left there */
+    hipLaunchKernelGGL(zero_words_kernel, dim3((u32)((groups + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, w.cnt, (u32)groups);
+    HIP_TRY(hipGetLastError());
+    TlWsFixed scope(&w);
+    RopeCfg rc0;
+    rope_cfg(L, nullptr, rc0);
+    return attn_core(L, a, true, rc0, (hipStream_t)stream);
 }
 
 static int decode_batch(const tl_decode_seq *seqs, uint32_t n_seq, uint32_t n_head,

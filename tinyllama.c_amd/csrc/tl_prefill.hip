@@ -93,6 +93,12 @@ int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &
     if (ns > max_ns) ns = max_ns;
     if (ns < 1) ns = 1;
     if (const u32 t = tl_tune(TL_TUNE_PREFILL_SPLITS)) ns = t;
+    if (const size_t fixed = tl_workspace_fixed_acc()) {
+        /* no-allocation call: as many key splits as the fixed region holds */
+        const size_t per_split = (size_t)a->n * a->n_head * D;
+        if ((size_t)ns * per_split > fixed) ns = (u32)(fixed / per_split);
+        if (ns < 1) ns = 1;
+    }
     p.n_split = ns;
     if (ns > 1) {
         TlWorkspace *w;

@@ -96,6 +96,7 @@ def lib():
         "tl_kv_copy_between": [ctypes.POINTER(KvLayer), ctypes.POINTER(KvLayer), u32, vp, vp,
                                u32, vp],
         "tl_attn": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs), vp],
+        "tl_attn_noalloc": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_noappend": [ctypes.POINTER(KvLayer), ctypes.POINTER(AttnArgs), vp],
         "tl_attn_decode_batch": [ctypes.POINTER(DecodeSeq), u32, u32, u32,
                                  ctypes.c_float, vp],
