@@ -836,6 +836,39 @@ def main():
                                  "reference's device layout) and without the fused append, "
                                  f"P = {pos} keys"}
 
+    # the same decode through a randomly permuted slot table (the layout
+    # after prefix reuse and eviction: every key's row is somewhere else in
+    # the pool); the rows hold the same kind of random data, so only the
+    # order of the reads changes
+    perm_steps = min(128, K)
+    g2 = torch.Generator(device="cpu")
+    g2.manual_seed(0x51A7)
+    perm = torch.randperm(cap, generator=g2).to(torch.int32).cuda()
+    args_p = [tlkv.attn_args(q[l], None, None, out[l], perm, pos - 1, 1, Hq, d, Hkv, 0, scale)
+              for l in range(L)]
+    for l in range(L):
+        tlkv.check(noapp(descs[l], args_p[l], sh))
+    torch.cuda.synchronize()
+    p0e, p1e = ev(), ev()
+    p0e.record(stream)
+    for _ in range(perm_steps):
+        for l in range(L):
+            rc = noapp(descs[l], args_p[l], sh)
+            if rc:
+                tlkv.check(rc)
+    p1e.record(stream)
+    torch.cuda.synchronize()
+    perm_us = p0e.elapsed_time(p1e) * 1e3 / (perm_steps * L)
+    perm_bytes = cont_bytes + pos * 4                   # + the slot-table reads
+    decode_permuted = {"us_per_layer_launch": round(perm_us, 3),
+                       "GBs": round(perm_bytes / (perm_us * 1e-6) / 1e9, 1),
+                       "hbm_frac": round(perm_bytes / (perm_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "steps": perm_steps,
+                       "note": "OP_ATTN (no append) through a random permutation of the "
+                               f"{cap}-row pool as slot table, P = {pos} keys; bytes include "
+                               "the slot-table reads"}
+    del perm
+
     # decode step with RoPE on q and the new k row (the reference's OP_ROPE x2
     # + OP_ATTN): three launches per layer (tl_rope, tl_rope, tl_attn) vs one
     # (tl_attn_rope), on raw (un-rotated) q/k rows; cache rows written past
@@ -898,6 +931,7 @@ def main():
                    "tok_s": round(K / (total_ms / 1e3), 1),
                    "frac_of_measured_ceiling": round(value / ceiling, 4)},
         "decode_contiguous": decode_contiguous,
+        "decode_permuted_slots": decode_permuted,
         "decode_with_rope_us_per_layer": {**rope_us, "steps": rope_steps,
                                           "note": "RoPE on q and the new k row each step: "
                                                   "tl_rope x2 + tl_attn vs tl_attn_rope"},
@@ -908,6 +942,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(),
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, read "
+                                       "from profiles/attn_decode_llama3-8b-32k_hbm_traffic.md "
+                                       "(not measured in this run)",
                      "kernel": "attn_decode_ring_kernel<128,4,false,false> (one OP_ATTN launch, "
                                "split merge inside)"},
     }

@@ -120,7 +120,9 @@ int tl_init(int device);
 #define TL_TUNE_DECODE_MERGE_KERNEL 2   /* 1: merge decode splits in a separate launch */
 #define TL_TUNE_PREFILL_SPLITS      3   /* key splits of the prefill kernel */
 #define TL_TUNE_NO_PREFILL          4   /* 1: run every batch on the decode kernel */
-#define TL_TUNE_COUNT               5
+#define TL_TUNE_DECODE_SINGLE_MERGE 5   /* 1: the last split of a group merges all of it */
+#define TL_TUNE_DECODE_MERGE_POLLS  6   /* n: at most n - 1 polls per wait of the split merge */
+#define TL_TUNE_COUNT               7
 int tl_set_tuning(int key, uint32_t value);
 uint32_t tl_get_tuning(int key);
 

@@ -294,18 +294,21 @@ def test_split_count_invariance(T):
 
 
 @pytest.mark.parametrize("shape", [(32, 8, 128, 8192, 8000), (28, 4, 128, 3000, 2900),
-                                   (32, 8, 64, 1024, 700), (8, 4, 256, 4096, 4000)])
+                                   (32, 8, 64, 1024, 700), (8, 4, 256, 4096, 4000),
+                                   (28, 4, 128, 8300, 8192), (8, 4, 256, 17000, 16384)])
 def test_decode_variants_agree(T, shape):
-    """In-launch split merge (last workgroup of a group) vs the separate merge
-    kernel: same result up to rounding, and each within tolerance of the
-    oracle."""
+    """The three ways of merging decode splits: every split merging a slice
+    of the output inside the launch (the default where it applies), the last
+    workgroup of a group merging all of it, and the separate merge kernel:
+    same result up to rounding, each within tolerance of the oracle."""
     n_head, n_kv, hd, cap, pos = shape
     import tlkv
     outs = []
-    for merge_kernel in (0, 1):
-        with tlkv.tuning(tlkv.TUNE_DECODE_MERGE_KERNEL, merge_kernel):
+    for merge_kernel, single in ((0, 0), (0, 1), (1, 0)):
+        with tlkv.tuning(tlkv.TUNE_DECODE_MERGE_KERNEL, merge_kernel), \
+                tlkv.tuning(tlkv.TUNE_DECODE_SINGLE_MERGE, single):
             out, o16, _, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, 1, 0, None, seed=pos)
-        assert np.abs(out - o16).max() < TOL, merge_kernel
+        assert np.abs(out - o16).max() < TOL, (merge_kernel, single)
         outs.append(out)
     for o in outs[1:]:
         assert np.abs(outs[0] - o).max() < 1e-4
@@ -641,3 +644,22 @@ def test_two_streams_interleaved_decode(T):
             ref = O.attn(S["C"], S["q"][t], S["k"][t], S["v"][t], S["slots"], pos0 + t, 1,
                          n_head)
             assert np.abs(host(S["out"][t]) - ref).max() < TOL, f"session {i} step {t}"
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128, 8192, 8000), (28, 4, 128, 8300, 8192)])
+def test_decode_split_merge_fallback(T, shape):
+    """The split merge's bounded waits, forced from the host: with no polls
+    every split gives up its slice and the last split of each group to
+    arrive merges all of them; with one poll some do and some do not.  The
+    outputs equal the default run's bit for bit (every slice is merged by
+    the same code from the same partials, whoever runs it)."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos = shape
+    outs = []
+    for polls in (0, 1, 2):
+        with tlkv.tuning(tlkv.TUNE_DECODE_MERGE_POLLS, polls):
+            out, o16, _, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, 1, 0, None, seed=pos)
+        assert np.abs(out - o16).max() < TOL, polls
+        outs.append(out)
+    for o in outs[1:]:
+        assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32))

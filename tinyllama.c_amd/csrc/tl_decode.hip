@@ -133,16 +133,34 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     p.chunk = chunk;
     p.n_split = n_split;
     p.counters = nullptr;
+    p.dist = 0;
     const bool in_kernel_merge = n_split > 1 && G * n_split <= 2048 &&
+                                 n_groups <= TL_MERGE_MAX_GROUPS &&
                                  !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL);
     if (n_split > 1) {
+        /* every split merges a slice of the output (dist) when there are
+         * enough splits to share the merge and all of the grid is resident
+         * at once (a split waits, bounded, for the rest of its group) */
+        const u64 resident = (u64)resident_per_cu(K.fn, K.threads) * cu_count();
+        p.dist = in_kernel_merge && n_split >= 24 && n_split <= TL_MERGE_MAX_SPLIT_DIST &&
+                 (u64)n_split * n_groups <= resident && !tl_tune(TL_TUNE_DECODE_SINGLE_MERGE);
         TlWorkspace *w;
         size_t parts = (size_t)n_rows_total * p.n_head * n_split;
-        int rc = tl_workspace_get(st, parts * head_dim, parts, in_kernel_merge ? n_groups : 0, &w);
+        /* dist: one (m, l, epoch) record of 16 bytes per partial */
+        int rc = tl_workspace_get(st, parts * head_dim, p.dist ? 2 * parts : parts,
+                                  in_kernel_merge ? TL_MERGE_CNT_WORDS : 0, &w);
         if (rc) return rc;
         p.ws_acc = w->acc;
         p.ws_ml = (float2 *)w->ml;
-        if (in_kernel_merge) p.counters = w->cnt;
+        if (in_kernel_merge) {
+            p.counters = w->cnt;
+            if (++w->epoch == 0) w->epoch = 2;   /* 0 is the tags' initial value */
+            p.epoch = w->epoch;
+            p.clear_n = w->hiwater;
+            const u32 polls = tl_tune(TL_TUNE_DECODE_MERGE_POLLS);
+            p.polls = polls ? polls - 1 : TL_MERGE_SPIN;
+            if (n_groups > w->hiwater) w->hiwater = (u32)n_groups;
+        }
     }
     void *args[] = {(void *)&p};
     HIP_TRY(hipLaunchKernel(K.fn, dim3(n_split * (u32)n_groups), dim3(K.threads), args, 0, st));

@@ -522,6 +522,56 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
     }
 }
 
+/* Bounded waits of the in-launch split merge (polls of device-coherent
+ * words, each a memory round trip): a split that waits longer gives up, and
+ * the last split to arrive merges what nobody else claimed. */
+#define TL_MERGE_SPIN 64
+#ifndef TL_MERGE_BACKOFF
+#define TL_MERGE_BACKOFF 4   /* s_sleep units (64 clocks) between polls */
+#endif
+
+/* Merge one slice of a group's output: columns [slice*cps, slice*cps + cps)
+ * of the G*D/4 float4 columns (head, 4 dims).  One wave per column, lane s
+ * holding split s (n_split <= 64): out = sum_s w_s acc_s / sum_s w_s l_s,
+ * w_s = exp2(m_s - max m).  Partial rows and their (m, l, epoch) records
+ * (float4 per partial) are read with device-coherent loads. */
+template <int D, int G, int W>
+TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq &sq,
+                        u32 slice, u32 cps) {
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    constexpr u32 COLS = G * D / 4;
+    const u32 ns = p.n_split;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const u32 c0 = slice * cps, c1 = min(c0 + cps, COLS);
+    const __amdgpu_buffer_rsrc_t rrec = buf_rsrc((const float4 *)p.ws_ml + pb);
+    const __amdgpu_buffer_rsrc_t racc = buf_rsrc(p.ws_acc + (u64)pb * D);
+    for (u32 col = c0 + (u32)wave; col < c1; col += W) {
+        const u32 h = col / (D / 4), d = (col % (D / 4)) * 4;
+        float m = NEG_INF, l = 0.f;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if ((u32)lane < ns) {
+            const u32 pi = h * ns + (u32)lane;
+            const u32x4v_t ml = __builtin_amdgcn_raw_buffer_load_b128(rrec, pi * 16, 0, TL_SC1);
+            const u32x4v_t v = __builtin_amdgcn_raw_buffer_load_b128(racc, (pi * D + d) * 4, 0, TL_SC1);
+            m = __uint_as_float(ml[0]);
+            l = __uint_as_float(ml[1]);
+            a = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                            __uint_as_float(v[3]));
+        }
+        const float M = group_max<64>(m);
+        const float mu = (M == NEG_INF) ? 0.f : M;
+        const float w = fast_exp2(m - mu);
+        const float L = group_sum<64>(w * l);
+        const float ox = group_sum<64>(w * a.x), oy = group_sum<64>(w * a.y);
+        const float oz = group_sum<64>(w * a.z), ow = group_sum<64>(w * a.w);
+        if (lane == 0) {
+            const float inv = 1.0f / L;
+            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)(kvh * G + h) * D + d] =
+                make_float4(ox * inv, oy * inv, oz * inv, ow * inv);
+        }
+    }
+}
+
 /* Decode attention with one workgroup of 8 waves per CU.  Each wave streams
  * its tiles (every 8th tile of the chunk) through a ring of two LDS stages
  * filled by LDS-direct loads: while one tile is computed the next is in
@@ -564,6 +614,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const int wave = tid >> 6;
     TL_TRACE(0);
     TL_TRACE_IDS();
+    if (p.counters) {
+        /* zero the other arrival bank for the next launch on this workspace */
+        u32 *other = p.counters + ((p.epoch & 1u) ^ 1u) * TL_MERGE_BANK_WORDS;
+        for (u32 i = blockIdx.x * NT + tid; i < p.clear_n; i += gridDim.x * NT)
+            other[i * TL_MERGE_PAD] = 0u;
+    }
 
     const u32 n_split = p.n_split;
     const u32 n_groups = gridDim.x / n_split;
@@ -839,6 +895,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     static_assert(HB * 4 * 64 <= WREG, "wave state exceeds its ring region");
     static_assert(GPW % TPC == 0, "lane groups per thread");
     __shared__ float s_lg[G][NGRP];
+    __shared__ float2 s_rec[G];
     float4 *s_w4 = (float4 *)&s_ring[0][0];
     const int sub = lane % LPK, gi = lane / LPK;
 #pragma unroll
@@ -920,10 +977,14 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                         u32x4v_t{__float_as_uint(O.x), __float_as_uint(O.y), __float_as_uint(O.z),
                                  __float_as_uint(O.w)},
                         buf_rsrc(p.ws_acc + (u64)pb * D), (pi * D + d) * 4, 0, TL_SC1);
-                    if (d == 0)
-                        __builtin_amdgcn_raw_buffer_store_b64(
-                            u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
-                            buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
+                    if (d == 0) {
+                        if (p.dist)
+                            s_rec[h] = make_float2(mm, L);   /* record written below */
+                        else
+                            __builtin_amdgcn_raw_buffer_store_b64(
+                                u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
+                                buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
+                    }
                 } else {
                     const u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
                     *(float4 *)&p.ws_acc[pi * D + d] = O;
@@ -934,20 +995,100 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     }
     if (single || !last_merges) return;
 
-    /* ---- the last split of this (row, kv-head) group to finish merges ----
-     * Its partial stores are complete (vmcnt 0) before the counter add, so
-     * the workgroup that sees n_split - 1 reads every partial. */
-    __shared__ u32 s_last;
+    /* ---- split merge ----
+     * A workgroup's partial stores are complete (vmcnt 0) before anything
+     * that announces them: its arrival in the group's counter and, in dist
+     * mode, the partials' (m, l, epoch, ~epoch) records.
+     * dist: the output columns of the group are cut into n_split slices and
+     * split i merges slice i once every record of its heads carries this
+     * launch's epoch (bounded wait), after tagging it as claimed; the last to
+     * arrive merges its own slice, then waits (bounded) for the other slices'
+     * claim tags and merges any slice still without one.  A slice merged
+     * twice gets the same bits twice.  Otherwise the last to arrive merges
+     * the whole group. */
+    __shared__ u32 s_last, s_flag;
+    __shared__ u64 s_todo;
     TL_TRACE(12);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     TL_TRACE(3);
+    u32 *arrive = p.counters + (p.epoch & 1u) * TL_MERGE_BANK_WORDS + grp * TL_MERGE_PAD;
+    if (p.dist) {
+        constexpr u32 COLS = G * D / 4;
+        const u32 cps = (COLS + n_split - 1) / n_split;   /* columns per slice */
+        const u32 c0 = split * cps, c1 = min(c0 + cps, COLS);
+        const __amdgpu_buffer_rsrc_t rrec = buf_rsrc((const float4 *)p.ws_ml + pb);
+        if (tid < G) {
+            const u32 pi = (u32)tid * n_split + split;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4v_t{__float_as_uint(s_rec[tid].x), __float_as_uint(s_rec[tid].y), p.epoch,
+                         ~p.epoch},
+                rrec, pi * 16, 0, TL_SC1);
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        if (tid == 64)   /* wave 1 counts the arrival while wave 0 polls */
+            s_last = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (wave == 0) {
+            u32 ok = c0 >= c1;   /* an empty slice needs nothing */
+            for (u32 it = 0; it < p.polls && !ok; it++) {
+                u64 missing = 0;
+                for (u32 h = c0 / (D / 4); h <= (c1 - 1) / (D / 4); h++) {
+                    bool have = true;
+                    if ((u32)lane < n_split) {
+                        const u32x4v_t rec = __builtin_amdgcn_raw_buffer_load_b128(
+                            rrec, (h * n_split + (u32)lane) * 16, 0, TL_SC1);
+                        have = rec[2] == p.epoch && rec[3] == ~p.epoch;
+                    }
+                    missing |= __builtin_amdgcn_ballot_w64(!have);
+                }
+                if (!missing) ok = 1;
+                else __builtin_amdgcn_s_sleep(TL_MERGE_BACKOFF);
+            }
+            if (lane == 0) s_flag = ok;
+        }
+        __syncthreads();
+        u32 *tags = p.counters + 2 * TL_MERGE_BANK_WORDS + grp * TL_MERGE_MAX_SPLIT_DIST;
+        const bool closer = s_last == n_split - 1;
+        if (!closer) {
+            if (!s_flag || c0 >= c1) return;                 /* the last to arrive covers it */
+            TL_TRACE(9);
+            /* claim the slice: from here this workgroup merges it unconditionally */
+            if (tid == 0)
+                __hip_atomic_store(&tags[split], p.epoch, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
+            TL_TRACE(4);
+            return;
+        }
+        TL_TRACE(9);
+        merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
+        /* slices whose owner has not claimed them (yet) */
+        if (wave == 0) {
+            u64 todo = 0;
+            for (u32 it = 0; it <= p.polls; it++) {
+                const u32 s = (u32)lane;
+                bool need = s < n_split && s != split && s * cps < COLS;
+                if (need)
+                    need = __hip_atomic_load(&tags[s], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) != p.epoch;
+                todo = __builtin_amdgcn_ballot_w64(need);
+                if (!todo || it == p.polls) break;
+                __builtin_amdgcn_s_sleep(TL_MERGE_BACKOFF);
+            }
+            if (lane == 0) s_todo = todo;
+        }
+        __syncthreads();
+        for (u64 todo = s_todo; todo; todo &= todo - 1)
+            merge_slice<D, G, W>(p, pb, r, kvh, sq, (u32)__builtin_ctzll(todo), cps);
+        TL_TRACE(4);
+        return;
+    }
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(&p.counters[grp], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
+        s_last = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (s_last != n_split - 1) return;
-    if (tid == 0) __hip_atomic_store(&p.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool closer = s_last == n_split - 1;
+    if (!closer) return;
     TL_TRACE(9);
     /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */
     split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0]);

@@ -103,7 +103,8 @@ static int ws_grow(TlWorkspace *w, size_t acc_floats, size_t ml_pairs, size_t co
         size_t cap = counters + 256;
         if (hipMalloc((void **)&w->cnt, cap * sizeof(u32)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu counters", cap);
-        /* Counters start at zero once; every launch leaves them at zero. */
+        /* Counters start at zero; the launches' bank and epoch rules keep
+         * them consistent from then on (tl_internal.h). */
         HIP_TRY(hipMemset(w->cnt, 0, cap * sizeof(u32)));
         HIP_TRY(hipDeviceSynchronize());
         w->cnt_cap = cap;
@@ -153,41 +154,51 @@ int tl_workspace_get(hipStream_t st, size_t acc_floats, size_t ml_pairs, size_t 
 /* One region per GPU for the whole process: split partials, (max, sum)
  * pairs and merge counters of tl_attn_noalloc.  Host code never uses the
  * symbol's name as an address: each device's copy sits at the address
- * hipGetSymbolAddress returns with that device current (g_scratch_dev). */
-#define TL_SCRATCH_ACC_FLOATS (30u << 18)   /* 30 MiB of partials */
+ * hipGetSymbolAddress returns with that device current (g_scratch_ws). */
+#define TL_SCRATCH_ACC_FLOATS (28u << 18)   /* 28 MiB of partials */
 #define TL_SCRATCH_ML_PAIRS (1u << 17)      /* 1 MiB of (max, sum) pairs */
-#define TL_SCRATCH_COUNTERS (1u << 18)      /* 1 MiB of merge counters */
+#define TL_SCRATCH_COUNTERS (3u << 18)      /* 3 MiB of merge counters */
+static_assert(TL_SCRATCH_COUNTERS >= TL_MERGE_CNT_WORDS, "scratch counters");
 #define TL_SCRATCH_BYTES                                                      \
     ((size_t)TL_SCRATCH_ACC_FLOATS * 4 + (size_t)TL_SCRATCH_ML_PAIRS * 8 +   \
      (size_t)TL_SCRATCH_COUNTERS * 4)
 static __device__ __align__(256) unsigned char scratch[TL_SCRATCH_BYTES];
-static unsigned char *g_scratch_dev[TL_MAX_DEV];
+static TlWorkspace g_scratch_ws[TL_MAX_DEV];   /* views of each device's region */
 static std::mutex g_scratch_mu;
 
-/* the calling thread's device's scratch address, set up on first use (the
- * counters zeroed once; every launch leaves them at zero) */
-static int scratch_setup(int dev, unsigned char **out) {
+/* the calling thread's device's scratch region, set up on first use: its
+ * address (hipGetSymbolAddress with the device current) and zeroed merge
+ * counters (launches keep them consistent from then on) */
+static int scratch_setup(int dev, TlWorkspace **out) {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (!g_scratch_dev[dev]) {
+    TlWorkspace *w = &g_scratch_ws[dev];
+    if (!w->acc) {
         void *ptr = nullptr;
         hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !ptr)
             return tl_fail(TL_EHIP, "scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
         unsigned char *base = (unsigned char *)ptr;
-        HIP_TRY(hipMemset(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4 +
-                              (size_t)TL_SCRATCH_ML_PAIRS * 8,
-                          0, (size_t)TL_SCRATCH_COUNTERS * 4));
+        u32 *cnt = (u32 *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4 +
+                           (size_t)TL_SCRATCH_ML_PAIRS * 8);
+        HIP_TRY(hipMemset(cnt, 0, (size_t)TL_SCRATCH_COUNTERS * 4));
         HIP_TRY(hipDeviceSynchronize());
-        g_scratch_dev[dev] = base;
+        w->acc = (float *)base;
+        w->ml = (float *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4);
+        w->cnt = cnt;
+        w->acc_cap = TL_SCRATCH_ACC_FLOATS;
+        w->ml_cap = TL_SCRATCH_ML_PAIRS;
+        w->cnt_cap = TL_SCRATCH_COUNTERS;
+        w->epoch = 0;
+        w->hiwater = 0;
     }
-    *out = g_scratch_dev[dev];
+    *out = w;
     return TL_OK;
 }
 
 extern "C" int tl_init(int device) {
     HIP_TRY(hipSetDevice(device));
     if (device < 0 || device >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", device);
-    unsigned char *sc;
+    TlWorkspace *sc;
     int rc = scratch_setup(device, &sc);
     if (rc) return rc;
     TlWorkspace *w;
@@ -204,7 +215,7 @@ static std::once_flag g_tune_once;
 static void tune_seed() {
     static const char *const names[TL_TUNE_COUNT] = {
         "TL_DECODE_WGS", "TL_DECODE_MIN_KEYS", "TL_DECODE_MERGE_KERNEL", "TL_PREFILL_SPLITS",
-        "TL_NO_PREFILL"};
+        "TL_NO_PREFILL", "TL_DECODE_SINGLE_MERGE", "TL_DECODE_MERGE_POLLS"};
     for (int i = 0; i < TL_TUNE_COUNT; i++) {
         const char *e = getenv(names[i]);
         g_tune[i].store(e && *e ? (u32)strtoul(e, NULL, 10) : 0u, std::memory_order_relaxed);
@@ -734,12 +745,6 @@ extern "C" int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, voi
     return attn_core(L, a, false, rc0, (hipStream_t)stream);
 }
 
-/* zero n words (the merge counters a launch will use) */
-__global__ __launch_bounds__(256) void zero_words_kernel(u32 *p, u32 n) {
-    for (u32 i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        p[i] = 0u;
-}
-
 extern "C" int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
     int rc = check_args(L, a);
     if (rc) return rc;
@@ -747,24 +752,10 @@ extern "C" int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", dev);
-    unsigned char *base;
-    rc = scratch_setup(dev, &base);
+    TlWorkspace *w;
+    rc = scratch_setup(dev, &w);
     if (rc) return rc;
-    TlWorkspace w;
-    w.acc = (float *)base;
-    w.ml = (float *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4);
-    w.cnt = (u32 *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4 + (size_t)TL_SCRATCH_ML_PAIRS * 8);
-    w.acc_cap = TL_SCRATCH_ACC_FLOATS;
-    w.ml_cap = TL_SCRATCH_ML_PAIRS;
-    w.cnt_cap = TL_SCRATCH_COUNTERS;
-    const u64 groups = (u64)a->n * L->n_kv_head;
-    if (groups > w.cnt_cap) return tl_fail(TL_ERANGE, "scratch: %llu row groups", (unsigned long long)groups);
-    /* the counters of this call start at zero whatever an earlier
-     * (overlapping) call left there */
-    hipLaunchKernelGGL(zero_words_kernel, dim3((u32)((groups + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, w.cnt, (u32)groups);
-    HIP_TRY(hipGetLastError());
-    TlWsFixed scope(&w);
+    TlWsFixed scope(w);
     RopeCfg rc0;
     rope_cfg(L, nullptr, rc0);
     return attn_core(L, a, true, rc0, (hipStream_t)stream);

@@ -56,7 +56,8 @@ class TlError(RuntimeError):
 
 # launch-shape overrides (include/tlkv.h TL_TUNE_*)
 TUNE_DECODE_WGS, TUNE_DECODE_MIN_KEYS, TUNE_DECODE_MERGE_KERNEL = 0, 1, 2
-TUNE_PREFILL_SPLITS, TUNE_NO_PREFILL = 3, 4
+TUNE_PREFILL_SPLITS, TUNE_NO_PREFILL, TUNE_DECODE_SINGLE_MERGE = 3, 4, 5
+TUNE_DECODE_MERGE_POLLS = 6
 
 
 class tuning:
