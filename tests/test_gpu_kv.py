@@ -663,3 +663,45 @@ def test_decode_split_merge_fallback(T, shape):
         outs.append(out)
     for o in outs[1:]:
         assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 128, 8200, 8000, 1), (32, 8, 128, 4200, 4000, 4)])
+def test_decode_graph_replay(T, shape):
+    """OP_ATTN captured in a HIP graph and replayed: each replay, with new q
+    written eagerly between replays, equals the eager call on the same
+    inputs bit for bit and the oracle within tolerance (the split merge's
+    state carries nothing from one replay into the next)."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n = shape
+    rng = np.random.default_rng(pos + n)
+    kd, qd = n_kv * hd, n_head * hd
+    L = tlkv.Layer(cap, n_kv, hd)
+    hk, hv = rows(rng, pos + n, kd), rows(rng, pos + n, kd)
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dev(T, hk)), tlkv.ptr(dev(T, hv)), kd,
+                                       None, 0, pos + n, None))
+    C = O.Cache(cap, n_kv, hd)
+    C.append(hk, hv, None, 0, pos + n)
+    dq = T.zeros((n, qd), dtype=T.float32, device="cuda")
+    out = T.zeros((n, qd), dtype=T.float32, device="cuda")
+    a = tlkv.attn_args(dq, None, None, out, None, pos, n, n_head, hd, n_kv, 0, O.scale_of(hd))
+    s = T.cuda.Stream()
+    sync(T)
+    for _ in range(2):      # workspace of the capture stream allocated before capture
+        tlkv.check(tlkv.lib().tl_attn_noappend(L.desc, a, s.cuda_stream))
+    s.synchronize()
+    g = T.cuda.CUDAGraph()
+    with T.cuda.graph(g, stream=s):
+        tlkv.check(tlkv.lib().tl_attn_noappend(L.desc, a, s.cuda_stream))
+    for i in range(4):
+        q = rows(rng, n, qd)
+        dq.copy_(T.from_numpy(q))
+        T.cuda.synchronize()
+        g.replay()
+        T.cuda.synchronize()
+        got = host(out).copy()
+        out.zero_()
+        tlkv.check(tlkv.lib().tl_attn_noappend(L.desc, a, None))
+        sync(T)
+        assert np.array_equal(got.view(np.uint32), host(out).view(np.uint32)), f"replay {i}"
+        ref = O.attn(C, q, hk[pos:], hv[pos:], None, pos, n, n_head)
+        assert np.abs(got - ref).max() < TOL, f"replay {i}"

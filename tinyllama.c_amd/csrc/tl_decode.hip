@@ -146,7 +146,7 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
                  (u64)n_split * n_groups <= resident && !tl_tune(TL_TUNE_DECODE_SINGLE_MERGE);
         TlWorkspace *w;
         size_t parts = (size_t)n_rows_total * p.n_head * n_split;
-        /* dist: one (m, l, epoch) record of 16 bytes per partial */
+        /* dist: one (m, l, epoch, ~epoch) record of 16 bytes per partial */
         int rc = tl_workspace_get(st, parts * head_dim, p.dist ? 2 * parts : parts,
                                   in_kernel_merge ? TL_MERGE_CNT_WORDS : 0, &w);
         if (rc) return rc;
@@ -154,12 +154,8 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
         p.ws_ml = (float2 *)w->ml;
         if (in_kernel_merge) {
             p.counters = w->cnt;
-            if (++w->epoch == 0) w->epoch = 2;   /* 0 is the tags' initial value */
-            p.epoch = w->epoch;
-            p.clear_n = w->hiwater;
             const u32 polls = tl_tune(TL_TUNE_DECODE_MERGE_POLLS);
             p.polls = polls ? polls - 1 : TL_MERGE_SPIN;
-            if (n_groups > w->hiwater) w->hiwater = (u32)n_groups;
         }
     }
     void *args[] = {(void *)&p};

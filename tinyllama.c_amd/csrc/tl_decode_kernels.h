@@ -614,12 +614,11 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const int wave = tid >> 6;
     TL_TRACE(0);
     TL_TRACE_IDS();
-    if (p.counters) {
-        /* zero the other arrival bank for the next launch on this workspace */
-        u32 *other = p.counters + ((p.epoch & 1u) ^ 1u) * TL_MERGE_BANK_WORDS;
-        for (u32 i = blockIdx.x * NT + tid; i < p.clear_n; i += gridDim.x * NT)
-            other[i * TL_MERGE_PAD] = 0u;
-    }
+    /* this launch's epoch (dist merge): read now, used at the end */
+    u32 epoch = 0;
+    if (p.dist && tid == 0)
+        epoch = __hip_atomic_load(p.counters + TL_MERGE_LAUNCHES, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) + 1u;
 
     const u32 n_split = p.n_split;
     const u32 n_groups = gridDim.x / n_split;
@@ -997,8 +996,9 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     /* ---- split merge ----
      * A workgroup's partial stores are complete (vmcnt 0) before anything
-     * that announces them: its arrival in the group's counter and, in dist
-     * mode, the partials' (m, l, epoch, ~epoch) records.
+     * that announces them: its arrival in the group's counter (which the
+     * last to arrive sets back to zero) and, in dist mode, the partials'
+     * (m, l, epoch, ~epoch) records.
      * dist: the output columns of the group are cut into n_split slices and
      * split i merges slice i once every record of its heads carries this
      * launch's epoch (bounded wait), after tagging it as claimed; the last to
@@ -1012,8 +1012,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     TL_TRACE(3);
-    u32 *arrive = p.counters + (p.epoch & 1u) * TL_MERGE_BANK_WORDS + grp * TL_MERGE_PAD;
+    u32 *arrive = p.counters + grp * TL_MERGE_PAD;
     if (p.dist) {
+        __shared__ u32 s_epoch;
+        if (tid == 0) s_epoch = epoch;
+        __syncthreads();
+        epoch = s_epoch;
         constexpr u32 COLS = G * D / 4;
         const u32 cps = (COLS + n_split - 1) / n_split;   /* columns per slice */
         const u32 c0 = split * cps, c1 = min(c0 + cps, COLS);
@@ -1021,8 +1025,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         if (tid < G) {
             const u32 pi = (u32)tid * n_split + split;
             __builtin_amdgcn_raw_buffer_store_b128(
-                u32x4v_t{__float_as_uint(s_rec[tid].x), __float_as_uint(s_rec[tid].y), p.epoch,
-                         ~p.epoch},
+                u32x4v_t{__float_as_uint(s_rec[tid].x), __float_as_uint(s_rec[tid].y), epoch,
+                         ~epoch},
                 rrec, pi * 16, 0, TL_SC1);
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
@@ -1038,7 +1042,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                     if ((u32)lane < n_split) {
                         const u32x4v_t rec = __builtin_amdgcn_raw_buffer_load_b128(
                             rrec, (h * n_split + (u32)lane) * 16, 0, TL_SC1);
-                        have = rec[2] == p.epoch && rec[3] == ~p.epoch;
+                        have = rec[2] == epoch && rec[3] == ~epoch;
                     }
                     missing |= __builtin_amdgcn_ballot_w64(!have);
                 }
@@ -1048,20 +1052,25 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             if (lane == 0) s_flag = ok;
         }
         __syncthreads();
-        u32 *tags = p.counters + 2 * TL_MERGE_BANK_WORDS + grp * TL_MERGE_MAX_SPLIT_DIST;
+        u32 *tags = p.counters + TL_MERGE_TAGS + grp * TL_MERGE_MAX_SPLIT_DIST;
         const bool closer = s_last == n_split - 1;
         if (!closer) {
             if (!s_flag || c0 >= c1) return;                 /* the last to arrive covers it */
             TL_TRACE(9);
             /* claim the slice: from here this workgroup merges it unconditionally */
             if (tid == 0)
-                __hip_atomic_store(&tags[split], p.epoch, __ATOMIC_RELAXED,
+                __hip_atomic_store(&tags[split], epoch, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
             TL_TRACE(4);
             return;
         }
         TL_TRACE(9);
+        if (tid == 0) {
+            __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(p.counters + TL_MERGE_LAUNCHES, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
         merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
         /* slices whose owner has not claimed them (yet) */
         if (wave == 0) {
@@ -1071,7 +1080,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                 bool need = s < n_split && s != split && s * cps < COLS;
                 if (need)
                     need = __hip_atomic_load(&tags[s], __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT) != p.epoch;
+                                             __HIP_MEMORY_SCOPE_AGENT) != epoch;
                 todo = __builtin_amdgcn_ballot_w64(need);
                 if (!todo || it == p.polls) break;
                 __builtin_amdgcn_s_sleep(TL_MERGE_BACKOFF);
@@ -1088,6 +1097,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         s_last = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const bool closer = s_last == n_split - 1;
+    if (closer && tid == 0)
+        __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!closer) return;
     TL_TRACE(9);
     /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */

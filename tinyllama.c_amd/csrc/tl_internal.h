@@ -56,25 +56,26 @@ struct DecParams {
     RopeCfg rope;            /* applied to q and to new K rows */
     uint32_t *counters;      /* merge counters (TL_MERGE_CNT_WORDS, layout below);
                                 NULL = partials are merged by attn_merge_kernel */
-    uint32_t epoch;          /* this launch's number on its workspace (never 0):
-                                arrival bank epoch & 1, done tags = epoch */
-    uint32_t clear_n;        /* groups of the other bank to zero (for the next launch) */
     uint32_t dist;           /* 1: every split merges its own slice of the output */
     uint32_t polls;          /* most polls per bounded wait of the split merge */
 };
 
-/* In-launch split merge counters, per workspace (u32 words):
- *   two banks of TL_MERGE_MAX_GROUPS arrival counts, one per (row, kv-head)
- *   group, each alone in a 128-byte line (TL_MERGE_PAD words); a launch
- *   counts in bank epoch & 1 and zeroes the first clear_n counts of the
- *   other bank, which the next launch uses;
- *   then TL_MERGE_MAX_SPLIT_DIST claim tags per group (a slice's merger
- *   writes the launch's epoch). */
+/* In-launch split merge state, per workspace (u32 words, zero at start):
+ *   [0, TL_MERGE_MAX_GROUPS * TL_MERGE_PAD): the arrival count of each
+ *     (row, kv-head) group, alone in a 128-byte line; the last split to
+ *     arrive sets it back to zero;
+ *   then TL_MERGE_MAX_SPLIT_DIST claim tags per group;
+ *   then the launch counter (its own line): every group's last split adds
+ *   one when a launch merges slices in every split (dist), and such a
+ *   launch reads it first: epoch = counter + 1 marks that launch's partial
+ *   records and claim tags.  Epochs never repeat on a workspace, also when
+ *   a captured graph replays the same launches. */
 #define TL_MERGE_MAX_GROUPS 4096
 #define TL_MERGE_PAD 32
 #define TL_MERGE_MAX_SPLIT_DIST 64
-#define TL_MERGE_BANK_WORDS (TL_MERGE_MAX_GROUPS * TL_MERGE_PAD)
-#define TL_MERGE_CNT_WORDS (2 * TL_MERGE_BANK_WORDS + TL_MERGE_MAX_SPLIT_DIST * TL_MERGE_MAX_GROUPS)
+#define TL_MERGE_TAGS (TL_MERGE_MAX_GROUPS * TL_MERGE_PAD)
+#define TL_MERGE_LAUNCHES (TL_MERGE_TAGS + TL_MERGE_MAX_SPLIT_DIST * TL_MERGE_MAX_GROUPS)
+#define TL_MERGE_CNT_WORDS (TL_MERGE_LAUNCHES + TL_MERGE_PAD)
 
 /* Chunked-prefill launch (one OP_ATTN batch of one session). */
 struct PrefParams {
@@ -97,8 +98,6 @@ struct TlWorkspace {
     float *ml;
     uint32_t *cnt;
     size_t acc_cap, ml_cap, cnt_cap;
-    uint32_t epoch;          /* launches with an in-launch merge so far */
-    uint32_t hiwater;        /* most groups any of them used */
 };
 
 /* A layer's storage as the attention launches read it: an f16 cache

@@ -103,8 +103,8 @@ static int ws_grow(TlWorkspace *w, size_t acc_floats, size_t ml_pairs, size_t co
         size_t cap = counters + 256;
         if (hipMalloc((void **)&w->cnt, cap * sizeof(u32)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu counters", cap);
-        /* Counters start at zero; the launches' bank and epoch rules keep
-         * them consistent from then on (tl_internal.h). */
+        /* The merge state starts at zero; launches keep it consistent
+         * from then on (tl_internal.h). */
         HIP_TRY(hipMemset(w->cnt, 0, cap * sizeof(u32)));
         HIP_TRY(hipDeviceSynchronize());
         w->cnt_cap = cap;
@@ -188,8 +188,6 @@ static int scratch_setup(int dev, TlWorkspace **out) {
         w->acc_cap = TL_SCRATCH_ACC_FLOATS;
         w->ml_cap = TL_SCRATCH_ML_PAIRS;
         w->cnt_cap = TL_SCRATCH_COUNTERS;
-        w->epoch = 0;
-        w->hiwater = 0;
     }
     *out = w;
     return TL_OK;
