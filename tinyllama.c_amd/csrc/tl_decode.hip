@@ -139,10 +139,11 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
                                  !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL);
     if (n_split > 1) {
         /* every split merges a slice of the output (dist) when there are
-         * enough splits to share the merge and all of the grid is resident
-         * at once (a split waits, bounded, for the rest of its group) */
+         * enough splits to share the merge (measured: with 8 or fewer the
+         * last split alone is faster) and all of the grid is resident at
+         * once (a split waits, bounded, for the rest of its group) */
         const u64 resident = (u64)resident_per_cu(K.fn, K.threads) * cu_count();
-        p.dist = in_kernel_merge && n_split >= 24 && n_split <= TL_MERGE_MAX_SPLIT_DIST &&
+        p.dist = in_kernel_merge && n_split >= 12 && n_split <= TL_MERGE_MAX_SPLIT_DIST &&
                  (u64)n_split * n_groups <= resident && !tl_tune(TL_TUNE_DECODE_SINGLE_MERGE);
         TlWorkspace *w;
         size_t parts = (size_t)n_rows_total * p.n_head * n_split;
