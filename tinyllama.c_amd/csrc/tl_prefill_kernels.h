@@ -129,8 +129,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     const u16 *Ksc = Q8 ? p.ks + (u64)kvh * p.cap * (D / 32) : nullptr;
     const u16 *Vsc = Q8 ? p.vs + (u64)kvh * p.cap * (D / 32) : nullptr;
 
-    /* register staging, AHEAD tiles ahead of the compute.  Unit u = tid + j*T
-     * -> row u / CPR, chunk u % CPR; rows past ke load zeros.  A Q8_0
+    /* register staging, AHEAD tiles ahead of the compute (and the slot
+     * table one tile further).  Unit u = tid + j*T -> row u / CPR, chunk
+     * u % CPR; rows past ke load zeros.  A Q8_0
      * cache's units are held raw (8 int8 and their block's scale) and
      * dequantized on the LDS write, with two register sets at head_dim
      * <= 128: a tile's loads are issued one iteration before the iteration
@@ -139,6 +140,23 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
      * no faster and costs occupancy at head_dim 64). */
     constexpr int AHEAD = (Q8 && D <= 128) ? 2 : 1;
     uint4 rk[AHEAD][UPT], rv[AHEAD][UPT];
+    /* physical rows of this thread's units of the next tile to load: read
+     * from the slot table one tile step before the tile's own loads, so the
+     * slot round trip never stalls a step */
+    u32 rows_next[UPT];
+    /* branch-free slot reads (buffer loads: offsets past the table, and every
+     * read when there is none, return 0), so nothing waits for them before
+     * their use a step later */
+    const __amdgpu_buffer_rsrc_t rslots = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)p.slots, (short)0, (p.slots && !p.ring) ? (int)(ke * 4u) : 0, 0x00020000);
+    auto fetch_rows = [&](u32 tb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < UPT; j++) {
+            const int u = tid + j * T;
+            const u32 key = tb + (u32)(u / CPR);
+            rows_next[j] = __builtin_amdgcn_raw_buffer_load_b32(rslots, key * 4u, 0, 0);
+        }
+    };
     auto load_tile = [&](u32 tb, int s) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
@@ -148,7 +166,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
             rk[s][j] = make_uint4(0, 0, 0, 0);
             rv[s][j] = make_uint4(0, 0, 0, 0);
             if (u < UNITS && key < ke) {
-                u32 ph = p.ring ? key % p.ring : (p.slots ? p.slots[key] : key);
+                u32 ph = p.ring ? key % p.ring : (p.slots ? rows_next[j] : key);
                 ph = ph < p.cap ? ph : 0;
                 if constexpr (Q8) {
                     const u64 e = (u64)ph * D + c * 8, sc = (u64)ph * (D / 32) + c / 4;
@@ -185,9 +203,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     const int tr_col = 16 * (gi & 1) + 4 * (li & 3);  /* + 32 b */
 
     if (ks < ke) {
+        fetch_rows(ks);
         load_tile(ks, 0);
         store_tile(0, 0);
-        if (AHEAD == 2 && ks + BN < ke) load_tile(ks + BN, AHEAD - 1);
+        if (ks + BN < ke) fetch_rows(ks + BN);
+        if (AHEAD == 2 && ks + BN < ke) {
+            load_tile(ks + BN, AHEAD - 1);
+            if (ks + 2 * BN < ke) fetch_rows(ks + 2 * BN);
+        }
     }
     __syncthreads();
     /* one tile: LDS buffer `buf` holds it, register set `sl` receives the
@@ -196,8 +219,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     auto tile_step = [&](u32 tb, int buf, int sl) __attribute__((always_inline)) {
         if constexpr (AHEAD == 2) {
             if (tb + 2 * BN < ke) load_tile(tb + 2 * BN, sl);
+            if (tb + 3 * BN < ke) fetch_rows(tb + 3 * BN);
         } else {
             if (tb + BN < ke) load_tile(tb + BN, 0);
+            if (tb + 2 * BN < ke) fetch_rows(tb + 2 * BN);
         }
         const uint4 *sk = s_k[buf];
         const _Float16 *sv_t = s_v[buf];
