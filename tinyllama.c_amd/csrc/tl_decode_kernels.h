@@ -876,33 +876,61 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     /* ---- one state per workgroup and head ----
      * The running max is wave-uniform, so the lanes of a wave add directly;
-     * the waves combine with weights exp2(m_w - M_h).  A wave that has
-     * finished its tiles writes its state into its own ring region (no
-     * barrier: that region is no longer read): acc as float4
-     * [head][k4][lane] (up to HB heads, 16 KB), l per lane group.  After
-     * one barrier, TPC threads per output float4 each add a share of the
-     * W * GPW lane groups (lanes sub + LPK*part: every 8-lane phase of a
-     * read touches distinct banks), then add across with shuffles.  More
-     * than HB heads take further rounds through the same memory. */
-    constexpr int GPW = 64 / LPK;                     /* lane groups per wave */
-    constexpr int NGRP = W * GPW;                     /* lane groups per workgroup */
-    constexpr int HB = G < 4 ? G : 4;                 /* heads per round */
-    constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
-    constexpr int TPC0 = NT / COLB > GPW ? GPW : NT / COLB;
-    constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
+     * the waves combine with weights exp2(m_w - M_h).  The lane groups of a
+     * DPP row are added in registers first; then a wave writes its state
+     * into its own ring region (no barrier: that region is no longer read):
+     * acc as float4 [head][k4][row-sum lane] (up to HB heads, 16 KB), l per
+     * remaining lane group.  After one barrier, TPC threads per output
+     * float4 each add a share of the W * GV lane groups (lanes sub +
+     * LPK*part: every 8-lane phase of a read touches distinct banks), then
+     * add across with shuffles.  More than HB heads take further rounds
+     * through the same memory. */
+    /* lane groups of one DPP row (16 lanes) are first added in registers
+     * (row rotations by 8, then 4), so only one group per row goes through
+     * LDS: PRE rotation steps, LV lanes per wave written, GV groups each */
+    constexpr int PRE = LPK == 8 ? 1 : LPK == 4 ? 2 : 0;
+    constexpr int LV = 64 >> PRE;
+    constexpr int GV = LV / LPK;                      /* lane groups per wave in LDS */
+    constexpr int NGRP = W * GV;                      /* lane groups per workgroup */
     constexpr int WREG = RING_U;                      /* float4 per wave region */
-    static_assert(HB * 4 * 64 <= WREG, "wave state exceeds its ring region");
-    static_assert(GPW % TPC == 0, "lane groups per thread");
+    constexpr int HB0 = WREG / (4 * LV);              /* heads that fit one round */
+    constexpr int HB = G < HB0 ? G : HB0;             /* heads per round */
+    constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
+    constexpr int TPC0 = NT / COLB > GV ? GV : NT / COLB;
+    constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
+    static_assert(HB * 4 * LV <= WREG, "wave state exceeds its ring region");
+    static_assert(GV % TPC == 0, "lane groups per thread");
+    if constexpr (PRE >= 1) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            l[h] += dpp_f<DPP_ROW_ROR8>(l[h]);
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[h][e] += dpp_f<DPP_ROW_ROR8>(acc[h][e]);
+        }
+    }
+    if constexpr (PRE >= 2) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            l[h] += dpp_f<DPP_ROW_ROR4>(l[h]);
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[h][e] += dpp_f<DPP_ROW_ROR4>(acc[h][e]);
+        }
+    }
+    /* lanes that hold their row's sums, and their place among them */
+    const bool vlane = (lane & (PRE == 2 ? 12 : PRE == 1 ? 8 : 0)) == 0;
+    const int ci = PRE == 0 ? lane : (lane % LPK) | ((lane >> 4) * LPK);
     __shared__ float s_lg[G][NGRP];
     __shared__ float2 s_rec[G];
     float4 *s_w4 = (float4 *)&s_ring[0][0];
-    const int sub = lane % LPK, gi = lane / LPK;
+    const int sub = lane % LPK, gv = ci / LPK;
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        if constexpr (own_head_softmax<G, LPK>()) {
-            if (sub == h) s_lg[h][wave * GPW + gi] = l[0];
-        } else {
-            if (sub == 0) s_lg[h][wave * GPW + gi] = l[h];
+        if (vlane) {
+            if constexpr (own_head_softmax<G, LPK>()) {
+                if (sub == h) s_lg[h][wave * GV + gv] = l[0];
+            } else {
+                if (sub == 0) s_lg[h][wave * GV + gv] = l[h];
+            }
         }
         if (lane == 0) s_m[wave][h] = m[h];
     }
@@ -916,14 +944,15 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     for (int h0 = 0; h0 < G; h0 += HB) {
         if (h0) __syncthreads();                      /* previous round read */
         float4 *mine = s_w4 + wave * WREG;
+        if (vlane)
 #pragma unroll
-        for (int hh = 0; hh < HB; hh++)
-            if (h0 + hh < G)
+            for (int hh = 0; hh < HB; hh++)
+                if (h0 + hh < G)
 #pragma unroll
-                for (int k4 = 0; k4 < 4; k4++)
-                    mine[(hh * 4 + k4) * 64 + lane] =
-                        make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
-                                    acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
+                    for (int k4 = 0; k4 < 4; k4++)
+                        mine[(hh * 4 + k4) * LV + ci] =
+                            make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
+                                        acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
         __syncthreads();
         if (h0 == 0) TL_TRACE(2);
         if (h0 == 0) TL_TRACE(8);
@@ -936,16 +965,16 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             const float mu = (mm == NEG_INF) ? 0.f : mm;
             float L = 0.f;
             float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 *src = s_w4 + (rhh * 4 + rk4) * 64 + rsub;
+            const float4 *src = s_w4 + (rhh * 4 + rk4) * LV + rsub;
 #pragma unroll
             for (int w = 0; w < W; w++) {
                 const float e = fast_exp2(s_m[w][h] - mu);
                 float lw = 0.f;
                 float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                for (int g = 0; g < GPW; g += TPC) {
+                for (int g = 0; g < GV; g += TPC) {
                     const float4 t = src[w * WREG + (g + rpart) * LPK];
-                    lw += s_lg[h][w * GPW + g + rpart];
+                    lw += s_lg[h][w * GV + g + rpart];
                     a.x += t.x; a.y += t.y; a.z += t.z; a.w += t.w;
                 }
                 L = fmaf(e, lw, L);
