@@ -266,9 +266,11 @@ static int append_only(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
         }
         const KvRequestState *req = tl_kv_cache_req(s->radix);
         if (req->len < pos + done) return fail(TL_ERANGE, "append: request map too short");
+        /* everything mapped so far, also positions a failed chunk mapped
+         * before failing: the change mark is consumed here */
         uint32_t lo = tl_kv_cache_take_dirty(s->radix);
-        if (lo != KV_SLOT_NONE && lo < pos + done) {
-            int rc = upload_slots(s, lo, pos + done);
+        if (lo != KV_SLOT_NONE && lo < req->len) {
+            int rc = upload_slots(s, lo, req->len);
             if (rc) return rc;
         }
     }
@@ -300,8 +302,8 @@ static int run_chunks(tl_session *s, const uint32_t *tokens, uint32_t n_tokens,
             const KvRequestState *req = tl_kv_cache_req(s->radix);
             if (req->len < p0 + chunk) return fail(TL_ERANGE, "execute: request map too short");
             uint32_t lo = tl_kv_cache_take_dirty(s->radix);
-            if (lo != KV_SLOT_NONE && lo < p0 + chunk) {
-                int rc = upload_slots(s, lo, p0 + chunk);
+            if (lo != KV_SLOT_NONE && lo < req->len) {
+                int rc = upload_slots(s, lo, req->len);
                 if (rc) return rc;
             }
         }
