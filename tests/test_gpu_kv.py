@@ -397,8 +397,11 @@ def test_prefill_split_invariance(T):
             out, o16, _, _, _ = _run_attn(T, 32, 8, 128, 2100, 1500, 512, 0, None, seed=21)
         assert np.abs(out - o16).max() < TOL
         outs.append(out)
-    assert np.abs(outs[0] - outs[1]).max() < 1e-4
-    assert np.abs(outs[0] - outs[2]).max() < 1e-4
+    # each split rounds its probabilities to f16 relative to its own running
+    # max reference (raised lazily, up to 2^8 below the true max), so split
+    # counts agree to f16 rounding of P, far inside the 2e-3 oracle bar
+    assert np.abs(outs[0] - outs[1]).max() < 3e-4
+    assert np.abs(outs[0] - outs[2]).max() < 3e-4
 
 
 @pytest.mark.parametrize("case", [

@@ -31,6 +31,11 @@ struct PCfg {
 
 TL_DEV half8_t h8_from_u4(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+TL_DEV half2_t pf_h2(u32 v) { return __builtin_bit_cast(half2_t, v); }
+
+#define TL_PF_RESCALE 8.0f /* lazy rescale threshold of the running max (log2) */
+
 TL_DEV u32 pack2(float a, float b) { return pack_f16x2_fast(a, b); }
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -119,7 +124,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     for (int b = 0; b < DB; b++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[b][r] = 0.f;
-    float m = NEG_INF, lsum = 0.f;
+    /* m: running max reference (NEG_INF until the row sees a key), mu: the
+     * same or 0, held negated in every bias lane */
+    float m = NEG_INF, mu = 0.f, lsum = 0.f;
+    floatx16_t bias = {};
+    const half2_t ones2 = {(_Float16)1.0f, (_Float16)1.0f};
 
     const u16 *Kb = p.k + (u64)kvh * p.cap * D;
     const u16 *Vb = p.v + (u64)kvh * p.cap * D;
@@ -149,6 +158,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
      * their use a step later */
     const __amdgpu_buffer_rsrc_t rslots = __builtin_amdgcn_make_buffer_rsrc(
         (void *)p.slots, (short)0, (p.slots && !p.ring) ? (int)(ke * 4u) : 0, 0x00020000);
+    /* this kv head's K and V rows as buffer resources (f16 cache; the
+     * launcher keeps cap * D * 2 within 32 bits, a multiple of 128, so at
+     * most 0xffffff80: below the 0xfffffff0 offset that marks a unit to
+     * zero-fill) */
+    const int head_bytes = (int)(u32)((u64)p.cap * D * 2);
+    const __amdgpu_buffer_rsrc_t rsk =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Kb, (short)0, head_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsv =
+        __builtin_amdgcn_make_buffer_rsrc((void *)Vb, (short)0, head_bytes, 0x00020000);
     auto fetch_rows = [&](u32 tb) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
@@ -163,6 +181,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
             const int u = tid + j * T;
             const int row = u / CPR, c = u % CPR;
             const u32 key = tb + row;
+            if constexpr (!Q8) {
+                /* buffer loads: an offset past the head's rows (the unit
+                 * beyond the tile, keys past ke, a slot past cap) reads 0 */
+                u32 ph = p.ring ? key % p.ring : (p.slots ? rows_next[j] : key);
+                const u32 off = (u < UNITS && key < ke && ph < p.cap) ? (ph * D + c * 8) * 2u
+                                                                      : 0xfffffff0u;
+                rk[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
+                rv[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
+                continue;
+            }
             rk[s][j] = make_uint4(0, 0, 0, 0);
             rv[s][j] = make_uint4(0, 0, 0, 0);
             if (u < UNITS && key < ke) {
@@ -227,15 +255,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
         const uint4 *sk = s_k[buf];
         const _Float16 *sv_t = s_v[buf];
 
-        /* S^T = K . Q^T per 32-key block: lane holds keys
+        /* S^T - mu = K . Q^T + bias per 32-key block (the accumulators start
+         * at -mu, this row's running reference): lane holds keys
          * 32 kb + 8(r/4) + 4h + r%4 of query lr */
         floatx16_t sacc[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) {
             const int krow = 32 * kb + lr;
-            const floatx16_t zero = {};
             sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                h8_from_u4(sk[krow * CPR + (h ^ (krow % CPR))]), qop[0], zero, 0, 0, 0);
+                h8_from_u4(sk[krow * CPR + (h ^ (krow % CPR))]), qop[0], bias, 0, 0, 0);
 #pragma unroll
             for (int s = 1; s < KS; s++) {
                 const int c = 2 * s + h;
@@ -245,7 +273,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
         }
 
         /* mask (only tiles that cross a boundary; visible keys of this lane's
-         * row are [klo, khi)) + online softmax */
+         * row are [klo, khi)) + online softmax.  The reference mu is raised
+         * only when the tile's max exceeds it by more than TL_PF_RESCALE
+         * (log2 units): then O and the sum are rescaled and the bias moved;
+         * otherwise P = 2^(s - mu) <= 2^TL_PF_RESCALE needs no subtraction */
         const bool full = tb + BN <= ke && tb + BN - 1 <= wq0 &&
                           (!p.window || tb + p.window > wq1);
         float sv[KB][16];
@@ -267,26 +298,31 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
         for (int kb = 0; kb < KB; kb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) mt = fmaxf(mt, sv[kb][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mn = fmaxf(m, mt);
-        const float mu = (mn == NEG_INF) ? 0.f : mn;
-        const float alpha = __builtin_amdgcn_exp2f(m - mu);
-        m = mn;
-        float ps = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < KB; kb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                sv[kb][r] = __builtin_amdgcn_exp2f(sv[kb][r] - mu);
-                ps += sv[kb][r];
+        mt = fmaxf(mt, __shfl_xor(mt, 32));          /* relative to mu */
+        const bool need = mt + mu > m + TL_PF_RESCALE;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+            const float d = need ? mt : 0.f;         /* new mu - mu */
+            const float alpha = (m == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(-d);
+            if (need) {
+                mu += d;
+                m = mu;
             }
-        lsum = lsum * alpha + ps;
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+            lsum *= alpha;
 #pragma unroll
             for (int b = 0; b < DB; b++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[b][r] *= alpha;
+#pragma unroll
+            for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) sv[kb][r] -= d;
+#pragma unroll
+            for (int r = 0; r < 16; r++) bias[r] = -mu;
         }
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) sv[kb][r] = __builtin_amdgcn_exp2f(sv[kb][r]);
 
         /* O^T += V^T . P^T per 16-key step; the MFMA's k = 8h + j maps to
          * keys 4h + j (j < 4) and 8 + 4h + (j - 4) of the step, the keys this
@@ -296,9 +332,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
 #pragma unroll
             for (int half = 0; half < 2; half++) {
                 const int r0 = 8 * half;
-                const half8_t pp = h8_from_u4(make_uint4(
+                const uint4 pu = make_uint4(
                     pack2(sv[kb][r0 + 0], sv[kb][r0 + 1]), pack2(sv[kb][r0 + 2], sv[kb][r0 + 3]),
-                    pack2(sv[kb][r0 + 4], sv[kb][r0 + 5]), pack2(sv[kb][r0 + 6], sv[kb][r0 + 7])));
+                    pack2(sv[kb][r0 + 4], sv[kb][r0 + 5]), pack2(sv[kb][r0 + 6], sv[kb][r0 + 7]));
+                const half8_t pp = h8_from_u4(pu);
+                /* the row sum of the f16 P the MFMA consumes */
+                lsum = __builtin_amdgcn_fdot2(pf_h2(pu.x), ones2, lsum, false);
+                lsum = __builtin_amdgcn_fdot2(pf_h2(pu.y), ones2, lsum, false);
+                lsum = __builtin_amdgcn_fdot2(pf_h2(pu.z), ones2, lsum, false);
+                lsum = __builtin_amdgcn_fdot2(pf_h2(pu.w), ones2, lsum, false);
                 const int kbase = 32 * kb + 16 * half + 4 * h + tr_row;
 #pragma unroll
                 for (int b = 0; b < DB; b++) {
