@@ -19,9 +19,14 @@
  *                                  between the two half-waves.
  *     online softmax in f32 (exp2); mask arithmetic only on tiles that cross
  *                                  the causal diagonal, the window edge or the
- *                                  range end; the O rescale is skipped when no
- *                                  row's max moved.  P^T is packed to f16
- *                                  straight from the accumulator registers.
+ *                                  range end.  Each row's reference mu moves
+ *                                  only when a tile's max passes it by more
+ *                                  than 2^8 (then O and the sum are rescaled);
+ *                                  -mu seeds the QK accumulators, so S - mu
+ *                                  leaves the MFMA as is.  P^T is packed to
+ *                                  f16 straight from the accumulator
+ *                                  registers; the row sum is a dot2 of the
+ *                                  packed P with (1, 1).
  *     O^T[d][row] += V^T . P^T     v_mfma_f32_32x32x16_f16 per 16 keys,
  *                                  A = V^T read from the row-major V tile with
  *                                  ds_read_b64_tr_b16 (a 4x16 -> 16x4 transpose
