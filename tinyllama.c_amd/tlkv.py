@@ -9,7 +9,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtlkv.so")
+# TLKV_LIB selects another build of the same library (e.g. the host-sanitizer
+# build, `make -C tinyllama.c_amd asan`)
+LIB_PATH = os.environ.get("TLKV_LIB") or os.path.join(HERE, "libtlkv.so")
 
 u32 = ctypes.c_uint32
 vp = ctypes.c_void_p
