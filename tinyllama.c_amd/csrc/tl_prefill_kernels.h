@@ -32,6 +32,7 @@ struct PCfg {
 TL_DEV half8_t h8_from_u4(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef u32 pf_u2v __attribute__((vector_size(8)));
 TL_DEV half2_t pf_h2(u32 v) { return __builtin_bit_cast(half2_t, v); }
 
 #define TL_PF_RESCALE 8.0f /* lazy rescale threshold of the running max (log2) */
@@ -162,11 +163,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
      * launcher keeps cap * D * 2 within 32 bits, a multiple of 128, so at
      * most 0xffffff80: below the 0xfffffff0 offset that marks a unit to
      * zero-fill) */
-    const int head_bytes = (int)(u32)((u64)p.cap * D * 2);
-    const __amdgpu_buffer_rsrc_t rsk =
-        __builtin_amdgcn_make_buffer_rsrc((void *)Kb, (short)0, head_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rsv =
-        __builtin_amdgcn_make_buffer_rsrc((void *)Vb, (short)0, head_bytes, 0x00020000);
+    const int head_bytes = (int)(u32)((u64)p.cap * D * (Q8 ? 1 : 2));
+    const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
+        Q8 ? (void *)K8 : (void *)Kb, (short)0, head_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
+        Q8 ? (void *)V8 : (void *)Vb, (short)0, head_bytes, 0x00020000);
+    /* Q8_0 scale planes: cap * D / 16 bytes per head */
+    const __amdgpu_buffer_rsrc_t rsks = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)Ksc, (short)0, Q8 ? (int)(p.cap * (D / 16)) : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsvs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)Vsc, (short)0, Q8 ? (int)(p.cap * (D / 16)) : 0, 0x00020000);
     auto fetch_rows = [&](u32 tb) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
@@ -189,22 +195,19 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
                                                                       : 0xfffffff0u;
                 rk[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
                 rv[s][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
-                continue;
-            }
-            rk[s][j] = make_uint4(0, 0, 0, 0);
-            rv[s][j] = make_uint4(0, 0, 0, 0);
-            if (u < UNITS && key < ke) {
-                u32 ph = p.ring ? key % p.ring : (p.slots ? rows_next[j] : key);
-                ph = ph < p.cap ? ph : 0;
-                if constexpr (Q8) {
-                    const u64 e = (u64)ph * D + c * 8, sc = (u64)ph * (D / 32) + c / 4;
-                    const uint2 kq = *(const uint2 *)(K8 + e), vq = *(const uint2 *)(V8 + e);
-                    rk[s][j] = make_uint4(kq.x, kq.y, Ksc[sc], 0);
-                    rv[s][j] = make_uint4(vq.x, vq.y, Vsc[sc], 0);
-                } else {
-                    rk[s][j] = *(const uint4 *)(Kb + (u64)ph * D + c * 8);
-                    rv[s][j] = *(const uint4 *)(Vb + (u64)ph * D + c * 8);
-                }
+            } else {
+                /* the same for the int8 values and their block's scale: a
+                 * unit out of range reads zero values and a zero scale */
+                const u32 ph = p.ring ? key % p.ring : (p.slots ? rows_next[j] : key);
+                const bool ok = u < UNITS && key < ke && ph < p.cap;
+                const u32 off = ok ? ph * D + c * 8 : 0xfffffff0u;
+                const u32 soff = ok ? (ph * (D / 32) + c / 4) * 2u : 0xfffffff0u;
+                const pf_u2v kq = __builtin_amdgcn_raw_buffer_load_b64(rsk, off, 0, 0);
+                const pf_u2v vq = __builtin_amdgcn_raw_buffer_load_b64(rsv, off, 0, 0);
+                const u32 ks = __builtin_amdgcn_raw_buffer_load_b16(rsks, soff, 0, 0);
+                const u32 vs = __builtin_amdgcn_raw_buffer_load_b16(rsvs, soff, 0, 0);
+                rk[s][j] = make_uint4(kq[0], kq[1], ks, 0);
+                rv[s][j] = make_uint4(vq[0], vq[1], vs, 0);
             }
         }
     };
