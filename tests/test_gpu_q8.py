@@ -185,6 +185,8 @@ Q8_CASES = [
     (16, 2, 128, 1200, 300, 200, 0, True, 0),    # prefill (MFMA, dequant on load)
     (8, 4, 256, 1500, 700, 64, 256, False, 0),   # prefill, windowed, head_dim 256
     (8, 1, 64, 600, 0, 333, 0, True, 0),         # prefill from empty
+    (28, 4, 128, 1200, 600, 100, 0, True, 0),    # prefill, gqa 7 (configs 2/3), ragged rows
+    (24, 8, 128, 900, 300, 64, 0, True, 0),      # prefill, gqa 3
 ]
 
 
