@@ -104,16 +104,17 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p, u32 
         float4 a[K];
 #pragma unroll
         for (int k = 0; k < K; k++) {
-            const u32 s = min(s0 + k, ns - 1);
-            ml[k] = p.ws_ml[pb + s];
-            a[k] = *(const float4 *)&p.ws_acc[(pb + s) * D + d];
+            /* splits past the last are not loaded (uniform branch) */
+            ml[k] = make_float2(NEG_INF, 0.f);
+            a[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (s0 + k < ns) {
+                ml[k] = p.ws_ml[pb + s0 + k];
+                a[k] = *(const float4 *)&p.ws_acc[(pb + s0 + k) * D + d];
+            }
         }
         float bm = NEG_INF;
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            if (s0 + k >= ns) ml[k] = make_float2(NEG_INF, 0.f);
-            bm = fmaxf(bm, ml[k].x);
-        }
+        for (int k = 0; k < K; k++) bm = fmaxf(bm, ml[k].x);
         const float nm = fmaxf(M, bm);
         const float mu = (nm == NEG_INF) ? 0.f : nm;
         const float sc = fast_exp2(M - mu);
