@@ -16,11 +16,12 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 TL_DEV half2_t as_h2(u32 w) { return __builtin_bit_cast(half2_t, w); }
 
 /* 8 f32 -> 8 binary16 (RNE, NaN pinned), the append conversion */
-TL_DEV uint4 cvt8_f16(const float *src) {
-    const float4 a = *(const float4 *)src;
-    const float4 b = *(const float4 *)(src + 4);
+TL_DEV uint4 cvt8_f16_regs(float4 a, float4 b) {
     return make_uint4(pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
                       pack_f16x2(b.z, b.w));
+}
+TL_DEV uint4 cvt8_f16(const float *src) {
+    return cvt8_f16_regs(*(const float4 *)src, *(const float4 *)(src + 4));
 }
 
 TL_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -615,11 +616,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const int wave = tid >> 6;
     TL_TRACE(0);
     TL_TRACE_IDS();
-    /* this launch's epoch (dist merge): read now, used at the end */
-    u32 epoch = 0;
-    if (p.dist && tid == 0)
-        epoch = __hip_atomic_load(p.counters + TL_MERGE_LAUNCHES, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    /* this launch's epoch (dist merge) is the launch counter + 1: the
+     * counter is read now (device-coherent, as the closers' increments are)
+     * and first used at the end, so nothing waits for it here */
+    const u32 launches = __builtin_amdgcn_raw_buffer_load_b32(
+        buf_rsrc(p.dist ? p.counters + TL_MERGE_LAUNCHES : nullptr), p.dist ? 0u : 0xfffffff0u, 0,
+        TL_SC1);                                   /* without dist: out of range, reads 0 */
 
     const u32 n_split = p.n_split;
     const u32 n_groups = gridDim.x / n_split;
@@ -650,11 +652,18 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     /* physical rows of the chunk's keys */
     const bool staged = (sq.ring == 0) && (sq.slots != nullptr);
-    if (staged)
-        for (u32 i = kbeg + tid; i < kend; i += NT) {
-            const u32 s = sq.slots[i];
-            s_slot[i - kbeg] = s < sq.cap ? s : 0u;
+    /* the chunk's slots are loaded here and stored to LDS after q and the new
+     * rows have been requested too, so the prologue waits for one round
+     * trip, not one per load */
+    constexpr int SPT = TL_DEC_MAX_CHUNK / NT;      /* slots per thread */
+    u32 slot_v[SPT];
+    if (staged) {
+#pragma unroll
+        for (int j = 0; j < SPT; j++) {
+            const u32 i = kbeg + tid + j * NT;
+            slot_v[j] = i < kend ? sq.slots[i] : 0u;
         }
+    }
     /* q of the GQA group (RoPE'd at pos + r when ROPE), scaled to log2 units,
      * f16; the launch's new K/V rows (K RoPE'd at pos + row), f16 */
     const float sc = p.scale_log2;
@@ -710,19 +719,39 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             }
         }
     } else {
-        for (int i = tid; i < G * D / 8; i += NT) {
-            const float4 a = *(const float4 *)(qb + i * 8);
-            const float4 b = *(const float4 *)(qb + i * 8 + 4);
-            s_q[i] = make_uint4(pack_f16x2_fast(a.x * sc, a.y * sc), pack_f16x2_fast(a.z * sc, a.w * sc),
-                                pack_f16x2_fast(b.x * sc, b.y * sc), pack_f16x2_fast(b.z * sc, b.w * sc));
+        /* one q item and at most one new-row item per thread (G * D / 8 and
+         * TL_DEC_MAX_NEW * D / 8 are at most NT): all loads first */
+        static_assert(G * D / 8 <= NT && TL_DEC_MAX_NEW * (D / 8) <= NT, "one item per thread");
+        float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qc = qa;
+        float4 ka = qa, kc = qa, va = qa, vc = qa;
+        const bool has_q = tid < G * D / 8;
+        const bool has_new = need_new && (u32)tid < p.rows_per_seq * VPR;
+        const u32 nrow = (u32)tid / VPR, nc8 = (u32)tid % VPR;
+        if (has_q) {
+            qa = *(const float4 *)(qb + tid * 8);
+            qc = *(const float4 *)(qb + tid * 8 + 4);
         }
-        if (need_new)
-            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
-                const u32 row = i / VPR, c8 = i % VPR;
-                const u64 src = (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8;
-                s_newk[row][c8] = cvt8_f16(sq.kin + src);
-                s_newv[row][c8] = cvt8_f16(sq.vin + src);
-            }
+        if (has_new) {
+            const u64 src = (u64)nrow * sq.kv_stride + (u64)kvh * D + nc8 * 8;
+            ka = *(const float4 *)(sq.kin + src);
+            kc = *(const float4 *)(sq.kin + src + 4);
+            va = *(const float4 *)(sq.vin + src);
+            vc = *(const float4 *)(sq.vin + src + 4);
+        }
+        if (has_q)
+            s_q[tid] = make_uint4(pack_f16x2_fast(qa.x * sc, qa.y * sc), pack_f16x2_fast(qa.z * sc, qa.w * sc),
+                                  pack_f16x2_fast(qc.x * sc, qc.y * sc), pack_f16x2_fast(qc.z * sc, qc.w * sc));
+        if (has_new) {
+            s_newk[nrow][nc8] = cvt8_f16_regs(ka, kc);
+            s_newv[nrow][nc8] = cvt8_f16_regs(va, vc);
+        }
+    }
+    if (staged) {
+#pragma unroll
+        for (int j = 0; j < SPT; j++) {
+            const u32 i = tid + j * NT;
+            if (kbeg + i < kend) s_slot[i] = slot_v[j] < sq.cap ? slot_v[j] : 0u;
+        }
     }
     __syncthreads();
     TL_TRACE(1);
@@ -1045,9 +1074,9 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     u32 *arrive = p.counters + grp * TL_MERGE_PAD;
     if (p.dist) {
         __shared__ u32 s_epoch;
-        if (tid == 0) s_epoch = epoch;
+        if (tid == 0) s_epoch = launches + 1u;
         __syncthreads();
-        epoch = s_epoch;
+        const u32 epoch = s_epoch;
         constexpr u32 COLS = G * D / 4;
         const u32 cps = (COLS + n_split - 1) / n_split;   /* columns per slice */
         const u32 c0 = split * cps, c1 = min(c0 + cps, COLS);
