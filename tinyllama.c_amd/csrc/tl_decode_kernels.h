@@ -668,55 +668,99 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
      * f16; the launch's new K/V rows (K RoPE'd at pos + row), f16 */
     const float sc = p.scale_log2;
     if constexpr (ROPE) {
+        /* pairs (ia, ib) of q and of the new K rows, rotated by position,
+         * and the new V rows: every thread requests its (few) items first,
+         * then rotates, converts and stores them */
+        constexpr int QI = (G * (D / 2) + NT - 1) / NT;                /* q pairs */
+        constexpr int KI = (TL_DEC_MAX_NEW * (D / 2) + NT - 1) / NT;   /* K pairs */
+        constexpr int VI = (TL_DEC_MAX_NEW * (D / 8) + NT - 1) / NT;   /* V 8-element units */
         const u32 pairs = p.rope.rdim >> 1;
-        u16 *q16 = (u16 *)s_q;
-        for (u32 t = tid; t < (u32)G * (D / 2); t += NT) {
-            const u32 h = t / (D / 2), i = t % (D / 2);
-            const float *row = qb + h * D;
-            u32 ia, ib;
-            float x, y;
-            if (i < pairs) {
-                ia = p.rope.neox ? i : 2 * i;
-                ib = p.rope.neox ? i + pairs : 2 * i + 1;
-                float c, sn;
-                rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
-                rope_rot(row[ia], row[ib], c, sn, x, y);
-            } else {
-                ia = 2 * i;
-                ib = 2 * i + 1;
-                x = row[ia];
-                y = row[ib];
-            }
-            const u32 pk = pack_f16x2_fast(x * sc, y * sc);
-            q16[h * D + ia] = (u16)(pk & 0xffffu);
-            q16[h * D + ib] = (u16)(pk >> 16);
-        }
-        if (need_new) {
-            for (u32 t = tid; t < p.rows_per_seq * (D / 2); t += NT) {
-                const u32 row = t / (D / 2), i = t % (D / 2);
-                const float *src = sq.kin + (u64)row * sq.kv_stride + (u64)kvh * D;
+        const u32 nkp = need_new ? p.rows_per_seq * (D / 2) : 0u;
+        const u32 nvu = need_new ? p.rows_per_seq * VPR : 0u;
+        /* element indices of pair i: rotated pairs per the RoPE variant,
+         * the rest (i >= pairs) stay adjacent */
+        auto pair_of = [&](u32 i, u32 &ia, u32 &ib) {
+            const bool rot = i < pairs;
+            ia = (rot && p.rope.neox) ? i : 2 * i;
+            ib = (rot && p.rope.neox) ? i + pairs : 2 * i + 1;
+        };
+        float qx[QI], qy[QI], kx[KI], ky[KI];
+        float4 va[VI], vc[VI];
+#pragma unroll
+        for (int j = 0; j < QI; j++) {
+            const u32 t = tid + j * NT;
+            qx[j] = qy[j] = 0.f;
+            if (t < (u32)G * (D / 2)) {
                 u32 ia, ib;
-                float x, y;
+                pair_of(t % (D / 2), ia, ib);
+                const float *row = qb + (t / (D / 2)) * D;
+                qx[j] = row[ia];
+                qy[j] = row[ib];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KI; j++) {
+            const u32 t = tid + j * NT;
+            kx[j] = ky[j] = 0.f;
+            if (t < nkp) {
+                u32 ia, ib;
+                pair_of(t % (D / 2), ia, ib);
+                const float *src = sq.kin + (u64)(t / (D / 2)) * sq.kv_stride + (u64)kvh * D;
+                kx[j] = src[ia];
+                ky[j] = src[ib];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < VI; j++) {
+            const u32 i = tid + j * NT;
+            va[j] = vc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < nvu) {
+                const float *src = sq.vin + (u64)(i / VPR) * sq.kv_stride + (u64)kvh * D + (i % VPR) * 8;
+                va[j] = *(const float4 *)src;
+                vc[j] = *(const float4 *)(src + 4);
+            }
+        }
+        u16 *q16 = (u16 *)s_q;
+#pragma unroll
+        for (int j = 0; j < QI; j++) {
+            const u32 t = tid + j * NT;
+            if (t < (u32)G * (D / 2)) {
+                const u32 h = t / (D / 2), i = t % (D / 2);
+                u32 ia, ib;
+                pair_of(i, ia, ib);
+                float x = qx[j], y = qy[j];
                 if (i < pairs) {
-                    ia = p.rope.neox ? i : 2 * i;
-                    ib = p.rope.neox ? i + pairs : 2 * i + 1;
+                    float c, sn;
+                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
+                    rope_rot(qx[j], qy[j], c, sn, x, y);
+                }
+                const u32 pk = pack_f16x2_fast(x * sc, y * sc);
+                q16[h * D + ia] = (u16)(pk & 0xffffu);
+                q16[h * D + ib] = (u16)(pk >> 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KI; j++) {
+            const u32 t = tid + j * NT;
+            if (t < nkp) {
+                const u32 row = t / (D / 2), i = t % (D / 2);
+                u32 ia, ib;
+                pair_of(i, ia, ib);
+                float x = kx[j], y = ky[j];
+                if (i < pairs) {
                     float c, sn;
                     rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + row, c, sn);
-                    rope_rot(src[ia], src[ib], c, sn, x, y);
-                } else {
-                    ia = 2 * i;
-                    ib = 2 * i + 1;
-                    x = src[ia];
-                    y = src[ib];
+                    rope_rot(kx[j], ky[j], c, sn, x, y);
                 }
                 u16 *k16 = (u16 *)s_newk[row];
                 k16[ia] = (u16)f32_to_f16_bits(x);
                 k16[ib] = (u16)f32_to_f16_bits(y);
             }
-            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
-                const u32 row = i / VPR, c8 = i % VPR;
-                s_newv[row][c8] = cvt8_f16(sq.vin + (u64)row * sq.kv_stride + (u64)kvh * D + c8 * 8);
-            }
+        }
+#pragma unroll
+        for (int j = 0; j < VI; j++) {
+            const u32 i = tid + j * NT;
+            if (i < nvu) s_newv[i / VPR][i % VPR] = cvt8_f16_regs(va[j], vc[j]);
         }
     } else {
         /* one q item and at most one new-row item per thread (G * D / 8 and
