@@ -411,6 +411,19 @@ class KvCache:
 
 # ---- session (include/tl_session.h) -------------------------------------------
 
+def _ptr_array(tensors, n):
+    """ctypes array of the n tensors' device addresses (each distinct tensor
+    asked once: callers often pass one buffer for every layer)."""
+    seen = {}
+    out = (vp * n)()
+    for i, t in enumerate(tensors):
+        a = seen.get(id(t))
+        if a is None:
+            a = seen[id(t)] = t.data_ptr()
+        out[i] = a
+    return out
+
+
 class SessionCfg(ctypes.Structure):
     _fields_ = [("n_layer", u32), ("n_head", u32), ("n_kv_head", u32), ("head_dim", u32),
                 ("ctx_size", u32), ("n_ubatch", u32), ("window", ctypes.POINTER(u32)),
@@ -514,15 +527,15 @@ class Session:
     def append(self, tokens, k, v, kv_stride):
         """K/V write-through only (per-layer device tensors [n_tokens][kv_stride])."""
         a, p = _u32_array(tokens)
-        arr = lambda ts: (vp * self.n_layer)(*[t.data_ptr() for t in ts])
-        check(self.L.tl_session_append(self.h, p, a.size, arr(k), arr(v), kv_stride))
+        check(self.L.tl_session_append(self.h, p, a.size, _ptr_array(k, self.n_layer),
+                                       _ptr_array(v, self.n_layer), kv_stride))
 
     def execute(self, tokens, q, k, v, out, q_stride, kv_stride):
         """q/k/v/out: per-layer device tensors [n_tokens][stride]."""
         a, p = _u32_array(tokens)
-        arr = lambda ts: (vp * self.n_layer)(*[t.data_ptr() for t in ts])
-        check(self.L.tl_session_execute(self.h, p, a.size, arr(q), arr(k), arr(v), arr(out),
-                                        q_stride, kv_stride))
+        n = self.n_layer
+        check(self.L.tl_session_execute(self.h, p, a.size, _ptr_array(q, n), _ptr_array(k, n),
+                                        _ptr_array(v, n), _ptr_array(out, n), q_stride, kv_stride))
 
     @property
     def pos(self):
