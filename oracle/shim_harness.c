@@ -111,8 +111,12 @@ int rh_attn_shim(const float *q, const float *k, const float *v, float *dst, voi
  * (graph_rope / graph_rope_norm params: theta bits, heads, head_dim,
  * rope_dim) -> OP_ATTN.  With `extra` set, one more node reads the rotated K,
  * so the shim must run the K rotation on its own.  q_rot / k_rot: device
- * buffers the RoPE nodes write when they run.  *fused receives the number of
- * OP_ATTN calls that fused their RoPE. */
+ * buffers the RoPE nodes write when they run.  Every node records its slot
+ * size in data_cap, as arena_plan does (src/graph.c:753-754); the caller may
+ * pass slots that alias as arena_plan can place them (dst == q_in: the
+ * OP_ATTN output on the Q projection's freed slot; k_rot == q_in: the K
+ * rotation there).  *fused receives the number of OP_ATTN calls that fused
+ * their RoPE. */
 int rh_layer_shim(const float *q_in, const float *k_in, const float *v, float *q_rot,
                   float *k_rot, float *dst, void *kc, void *vc, u32 cap, void *radix, u32 pos,
                   u32 n, u32 n_head, u32 n_kv, u32 hd, u32 win, int neox, float theta,
@@ -142,6 +146,8 @@ int rh_layer_shim(const float *q_in, const float *k_in, const float *v, float *q
     ex.src[0] = &rk; ex.src[1] = &rk;
     link_nodes(&r, all, extra ? 7 : 6);
     const u32 qd = n_head * hd, kd = n_kv * hd;
+    nq.data_cap = rq.data_cap = at.data_cap = (size_t)n * qd * sizeof(float);
+    nk.data_cap = nv.data_cap = rk.data_cap = (size_t)n * kd * sizeof(float);
     unsigned f0 = hip_graph_op_fused_count();
     OpCtx c1 = ctx_for(&r, &rq, qd, pos, n);
     OpCtx c2 = ctx_for(&r, &rk, kd, pos, n);

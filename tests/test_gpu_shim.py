@@ -3,24 +3,25 @@ binding a tinyllama.c build uses: the reference's own OpCtx / Graph /
 GraphPlan / KvCache structs, built as graph_compute builds them, and a prefix
 cache made by libtlkv's kv_cache_create / match / append.
 
-- OP_ATTN through the shim matches the compiled reference's
-  cpu_graph_op(OP_ATTN) reading the same libtlkv cache through the
-  reference's header (within 2e-3), over multi-chunk request streams with
-  prefix hits and LRU evictions; the shim uploads the slot table itself;
+- OP_ATTN through the shim matches op_attn (src/backend/cpu/cpu_op.c:964-1064,
+  restated in oracle/oracle.c and pinned there against the compiled
+  reference) over the request's slot map read from the same libtlkv cache
+  (within 2e-3), over multi-chunk request streams with prefix hits and LRU
+  evictions; the shim uploads the slot table itself;
 - the batch rows land at the request's slots, f16 RNE, bit for bit, and
   AttnKvCache.n = pos + n (src/backend/cpu/cpu_op.c:995-1009);
 - RoPE nodes feeding only OP_ATTN are fused (same bits as running them on
-  their own) and the result matches the reference's OP_ROPE_* + OP_ATTN;
+  their own) and the result matches OP_ROPE_* (cpu_op.c:637-700) + OP_ATTN;
 - other ops go on to the device backend's gpu_graph_op (a CPU test).
-Needs oracle/_ref (built where the reference tree exists; it travels with the
-repository)."""
+Needs oracle/_ref/libtlshim.so: the product shim and its harness, compiled
+against the reference's headers (def.h, kvcache.h) where the reference tree
+exists; it holds no reference code and travels with the repository."""
 import numpy as np
 import pytest
 
 import oracle as O
 
-_built = pytest.mark.skipif(not (O.shim_available() and O.ref_available()),
-                            reason="executor shim / compiled reference not built")
+_built = pytest.mark.skipif(not O.shim_available(), reason="executor shim not built")
 
 
 @pytest.fixture(scope="module")
@@ -32,11 +33,12 @@ def T():
     return torch
 
 
-def _f32_cache(L, n_kv, cap, hd):
-    """the device f16 cache as f32 rows (the reference's f32 cache holding them)"""
-    kc = O.f16_to_f32(L.k.cpu().numpy().view(np.uint16)).reshape(n_kv, cap, hd)
-    vc = O.f16_to_f32(L.v.cpu().numpy().view(np.uint16)).reshape(n_kv, cap, hd)
-    return np.ascontiguousarray(kc), np.ascontiguousarray(vc)
+def _host_cache(L, n_kv, cap, hd):
+    """the oracle's f16 cache holding a copy of the device cache's bits"""
+    C = O.Cache(cap, n_kv, hd)
+    C.k[...] = L.k.cpu().numpy().view(np.uint16).reshape(n_kv, cap, hd)
+    C.v[...] = L.v.cpu().numpy().view(np.uint16).reshape(n_kv, cap, hd)
+    return C
 
 
 @_built
@@ -67,11 +69,9 @@ def test_shim_contiguous_matches_reference(T, nh, nkv, hd, cap, pos, n, win):
                                win, n_after.ctypes.data)
     T.cuda.synchronize()
     assert rc == 0 and int(n_after[0]) == pos + n
-    kc = np.zeros((nkv, cap, hd), np.float32)
-    vc = np.zeros_like(kc)
-    kc[:, :pos] = hk.reshape(pos, nkv, hd).transpose(1, 0, 2)
-    vc[:, :pos] = hv.reshape(pos, nkv, hd).transpose(1, 0, 2)
-    ref = O.ref_attn(kc, vc, q, k, v, None, pos, n, nh, window=win)
+    C = O.Cache(cap, nkv, hd)
+    C.append(hk, hv, None, 0, pos)
+    ref = O.attn(C, q, k, v, None, pos, n, nh, window=win)
     assert np.abs(out.cpu().numpy() - ref).max() < 2e-3
     got = L.k.cpu().numpy().view(np.uint16)[:, pos:pos + n].transpose(1, 0, 2).reshape(n, -1)
     assert np.array_equal(got, O.f16_bits(k))
@@ -110,7 +110,7 @@ def test_shim_over_libtlkv_radix_stream(T, seed, nh, nkv, hd, ctx, ub, win):
                 q = rng.standard_normal((n, qd)).astype(np.float32)
                 k = rng.standard_normal((n, kd)).astype(np.float32)
                 v = rng.standard_normal((n, kd)).astype(np.float32)
-                kc, vc = _f32_cache(L, nkv, ctx, hd)     # the cache before this op
+                C = _host_cache(L, nkv, ctx, hd)     # the cache before this op
                 dq, dk, dv = (T.from_numpy(x).cuda() for x in (q, k, v))
                 out = T.zeros((n, qd), dtype=T.float32, device="cuda")
                 n_after = np.zeros(1, dtype=np.uint32)
@@ -120,7 +120,7 @@ def test_shim_over_libtlkv_radix_stream(T, seed, nh, nkv, hd, ctx, ub, win):
                                            n_after.ctypes.data)
                 T.cuda.synchronize()
                 assert rc == 0 and int(n_after[0]) == p + n, f"req {req} pos {p}"
-                ref = O.ref_attn_radix(kv.h, kc, vc, q, k, v, p, n, nh, window=win)
+                ref = O.attn(C, q, k, v, kv.slots(p + n), p, n, nh, window=win)
                 err = np.abs(out.cpu().numpy() - ref).max()
                 assert err < 2e-3, f"req {req} pos {p} n {n}: {err}"
                 sl = kv.slots(p + n)[p:]
@@ -153,7 +153,11 @@ def test_shim_rope_fusion(T, neox, theta, nh, nkv, hd, rdim, pos, n):
     k = rng.standard_normal((n, kd)).astype(np.float32)
     v = rng.standard_normal((n, kd)).astype(np.float32)
     results = []
-    for extra in (0, 1):
+    # separate slots; a second reader of the rotated K; the OP_ATTN output on
+    # the Q projection's slot; the K rotation on the Q projection's slot (the
+    # last two as arena_plan can place them, src/graph.c:671-724)
+    for mode in ("separate", "extra", "dst_on_q", "krot_on_q"):
+        extra = int(mode == "extra")
         kv = tlkv.KvCache(cap)
         try:
             assert kv.match(toks) == 0
@@ -164,11 +168,11 @@ def test_shim_rope_fusion(T, neox, theta, nh, nkv, hd, rdim, pos, n):
             dhk, dhv = T.from_numpy(hk).cuda(), T.from_numpy(hv).cuda()
             tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dhk), tlkv.ptr(dhv), kd,
                                                tlkv.ptr(d_sl), 0, pos, None))
-            kc, vc = _f32_cache(L, nkv, cap, hd)
+            C = _host_cache(L, nkv, cap, hd)
             dq, dk, dv = (T.from_numpy(x).cuda() for x in (q, k, v))
             qr = T.zeros_like(dq)
-            kr = T.zeros_like(dk)
-            out = T.zeros((n, qd), dtype=T.float32, device="cuda")
+            kr = dq if mode == "krot_on_q" else T.zeros_like(dk)
+            out = dq if mode == "dst_on_q" else T.zeros((n, qd), dtype=T.float32, device="cuda")
             fused = np.zeros(1, dtype=np.uint32)
             rc = O.shim().rh_layer_shim(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                         qr.data_ptr(), kr.data_ptr(), out.data_ptr(),
@@ -177,22 +181,24 @@ def test_shim_rope_fusion(T, neox, theta, nh, nkv, hd, rdim, pos, n):
                                         fused.ctypes.data)
             T.cuda.synchronize()
             assert rc == 0
-            assert int(fused[0]) == (0 if extra else 1)
-            # the reference: OP_ROPE_* on q and k, then OP_ATTN over the same cache
-            rq = O.ref_rope(q, nh, hd, rdim, pos, theta, neox)
-            rk = O.ref_rope(k, nkv, hd, rdim, pos, theta, neox)
-            ref = O.ref_attn_radix(kv.h, kc, vc, rq, rk, v, pos, n, nh)
+            # fused only when both RoPE sources outlive the walk up to OP_ATTN
+            assert int(fused[0]) == (1 if mode == "separate" else 0), mode
+            # OP_ROPE_* on q and k, then OP_ATTN over the same cache
+            rq = O.rope(q, nh, hd, rdim, pos, theta, neox)
+            rk = O.rope(k, nkv, hd, rdim, pos, theta, neox)
+            ref = O.attn(C, rq, rk, v, sl, pos, n, nh)
             o = out.cpu().numpy()
-            assert np.abs(o - ref).max() < 2e-3
+            assert np.abs(o - ref).max() < 2e-3, mode
             rows = L.k.cpu().numpy().view(np.uint16)[:, sl[pos:]]
             results.append((o, rows))
             if extra:   # the rotated K was materialised for its other reader
                 assert np.abs(kr.cpu().numpy() - rk).max() < 1e-3
         finally:
             O.shim().rh_shim_release(kv.h)
-    # fused and unfused: the same bits
-    assert np.array_equal(results[0][0].view(np.uint32), results[1][0].view(np.uint32))
-    assert np.array_equal(results[0][1], results[1][1])
+    # fused and unfused, on any slots: the same bits
+    for o, rows in results[1:]:
+        assert np.array_equal(results[0][0].view(np.uint32), o.view(np.uint32))
+        assert np.array_equal(results[0][1], rows)
 
 
 @_built

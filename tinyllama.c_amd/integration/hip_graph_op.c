@@ -32,8 +32,15 @@
  * or K (n_kv_head heads), is not run on its own; the OP_ATTN of that layer
  * then reads the RoPE inputs and rotates them in its own launch
  * (tl_attn_rope: same results as the rotation followed by the attention,
- * bit for bit).  Other RoPE nodes run out of place as op_rope_norm /
- * op_rope_neox do (cpu_op.c:653-700): copy the rows, rotate them (tl_rope).
+ * bit for bit).  The fused launch reads the RoPE node's source later than
+ * the walk would, so a RoPE node is held back only when no node that runs
+ * between it and the OP_ATTN — the OP_ATTN's own output included — holds an
+ * arena slot overlapping that source: arena_plan (src/graph.c:671-724)
+ * frees a slot right after its last consumer runs, and for the Q / K
+ * projection that consumer is the RoPE node, so the OP_ATTN output (same
+ * size as Q) is often placed on the Q projection's slot.  Other RoPE nodes
+ * run out of place as op_rope_norm / op_rope_neox do (cpu_op.c:653-700):
+ * copy the rows, rotate them (tl_rope).
  *
  * Errors return false (the executor's goto fail path), never exit.  Like
  * the reference's device backend, the shim keeps process-global state
@@ -143,6 +150,27 @@ static bool attn_rope_pair(const OpCtx *c, const GraphNode *attn) {
     return true;
 }
 
+/* bytes [a, a + an) and [b, b + bn) share at least one byte */
+static bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return an && bn && x < y + bn && y < x + an;
+}
+
+/* The `bytes` read from rope->src[0] stay intact until `attn` has run: no
+ * node after `rope` up to and including `attn` writes an arena slot that
+ * overlaps them (node->data_cap bytes at node->data, src/graph.c:753-754;
+ * a node with data but no recorded size counts as overlapping). */
+static bool source_outlives(const GraphNode *rope, const GraphNode *attn, size_t bytes) {
+    const void *src = rope->src[0] ? rope->src[0]->data : NULL;
+    if (!src) return false;
+    for (const GraphNode *it = rope->next; it; it = it->next) {
+        if (it->data && (!it->data_cap || overlaps(it->data, it->data_cap, src, bytes)))
+            return false;
+        if (it == attn) return true;
+    }
+    return false;   /* attn not after rope */
+}
+
 static int deferred_index(const GraphNode *node, u32 pos, u32 n) {
     for (int i = 0; i < SHIM_MAX_DEFERRED; i++)
         if (g_deferred[i].node == node && g_deferred[i].pos == pos && g_deferred[i].n == n)
@@ -189,7 +217,8 @@ static bool op_rope(OpCtx *c) {
     const GraphNode *only = NULL;
     if (c->base == 0 && c->r == c->n && consumers(c->g, c->node, &only) == 1 &&
         only->op == OP_ATTN && attn_rope_pair(c, only) &&
-        c->od == (c->node == only->src[0] ? c->q_dim : c->kv_dim) && defer_rope(c))
+        c->od == (c->node == only->src[0] ? c->q_dim : c->kv_dim) &&
+        source_outlives(c->node, only, (size_t)c->n * c->od * sizeof(float)) && defer_rope(c))
         return true;   /* rotated inside that layer's OP_ATTN */
     return run_rope(c->node, c->dst, c->od, c->r, c->base, c->pos);
 }
