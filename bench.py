@@ -22,9 +22,9 @@ One JSON line is printed; besides the contract fields:
                 algorithmic bytes per launch / average launch time, the timed
                 region's HIP-event time on the launch stream over its K x 32
                 back-to-back launches
-  cpu_baseline  the reference's own op_attn (oracle/_ref, compiled from the
-                reference sources) timed on a bounded sample of the same
-                decode step, single thread
+  cpu_baseline  op_attn as the C restatement oracle/oracle.c runs it (the
+                reference's own objects do not travel to the GPU box) timed on
+                a bounded sample of the same decode step, single thread
   prefill, append, hbm_read_ceiling   the other measured rows
 """
 import argparse
@@ -67,15 +67,23 @@ def prefill_flops(c, p0, n):
     return 4 * c["Hq"] * c["d"] * keys
 
 
+def _port_cache(c, P, rng):
+    import oracle as O
+    C = O.Cache(P, c["Hkv"], c["d"], f16=False)
+    C.k = rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32)
+    C.v = rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32)
+    return C
+
+
 def cpu_baseline(c, P, n_layers_sample):
-    """The reference op_attn (compiled reference, f32 cache, one thread) on
-    `n_layers_sample` layers of one decode step at P keys."""
+    """op_attn (src/backend/cpu/cpu_op.c:964-1064) as the C restatement
+    oracle/oracle.c runs it (pinned against the compiled reference; it is the
+    only baseline that travels), f32 cache, one thread, on `n_layers_sample`
+    layers of one decode step at P keys."""
     import oracle as O
     rng = np.random.default_rng(7)
-    kind = "reference" if O.ref_available() else "port"
     kd = c["Hkv"] * c["d"]
-    kc = rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32)
-    vc = rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32)
+    C = _port_cache(c, P, rng)
     slots = np.arange(P, dtype=np.uint32)
     secs = 0.0
     for _ in range(n_layers_sample):
@@ -83,55 +91,47 @@ def cpu_baseline(c, P, n_layers_sample):
         k = rng.standard_normal((1, kd), dtype=np.float32)
         v = rng.standard_normal((1, kd), dtype=np.float32)
         t0 = time.perf_counter()
-        if kind == "reference":
-            O.ref_attn(kc, vc, q, k, v, slots, P - 1, 1, c["Hq"])
-        else:
-            C = O.Cache(P, c["Hkv"], c["d"], f16=False)
-            C.k, C.v = kc, vc
-            O.attn(C, q, k, v, slots, P - 1, 1, c["Hq"])
+        O.attn(C, q, k, v, slots, P - 1, 1, c["Hq"])
         secs += time.perf_counter() - t0
     per_layer = secs / n_layers_sample
     gbs = decode_bytes(c, P) / per_layer / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{n_layers_sample} layer calls of one decode step at P={P} "
-                      f"(op_attn over an f32 cache, single thread, {os.cpu_count()} host "
-                      f"cores present), {per_layer * 1e3:.1f} ms per layer; GB/s counts "
-                      f"the f16 workload's algorithmic bytes"}
+                      f"(op_attn restated in C, oracle/oracle.c, over an f32 cache, single "
+                      f"thread, {os.cpu_count()} host cores present), {per_layer * 1e3:.1f} ms "
+                      f"per layer; GB/s counts the f16 workload's algorithmic bytes"}
 
 
 def cpu_baseline_sessions(c, P, n_sessions, calls):
-    """The reference op_attn for `n_sessions` concurrent sessions, one host
-    thread each (the CPU server's -np N), `calls` decode-layer calls per
+    """op_attn (the C restatement) for `n_sessions` concurrent sessions, one
+    host thread each (the CPU server's -np N), `calls` decode-layer calls per
     session at P keys; aggregate GB/s of the f16 workload's algorithmic bytes
     over the wall time of the parallel section (ctypes releases the GIL)."""
-    import oracle as O
     from concurrent.futures import ThreadPoolExecutor
-    if not O.ref_available():
-        return None
+    import oracle as O
     kd = c["Hkv"] * c["d"]
     slots = np.arange(P, dtype=np.uint32)
     data = []
     for i in range(n_sessions):
         rng = np.random.default_rng(100 + i)
-        data.append((rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32),
-                     rng.standard_normal((c["Hkv"], P, c["d"]), dtype=np.float32),
+        data.append((_port_cache(c, P, rng),
                      rng.standard_normal((calls, c["Hq"] * c["d"]), dtype=np.float32),
                      rng.standard_normal((calls, kd), dtype=np.float32)))
 
     def work(i):
-        kc, vc, q, k = data[i]
+        C, q, k = data[i]
         for j in range(calls):
-            O.ref_attn(kc, vc, q[j:j + 1], k[j:j + 1], k[j:j + 1], slots, P - 1, 1, c["Hq"])
+            O.attn(C, q[j:j + 1], k[j:j + 1], k[j:j + 1], slots, P - 1, 1, c["Hq"])
 
     with ThreadPoolExecutor(n_sessions) as ex:
         t0 = time.perf_counter()
         list(ex.map(work, range(n_sessions)))
         secs = time.perf_counter() - t0
     gbs = n_sessions * calls * decode_bytes(c, P) / secs / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": n_sessions, "kind": "reference",
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": n_sessions, "kind": "port",
             "sample": f"{n_sessions} sessions on {n_sessions} threads, {calls} decode-layer "
-                      f"op_attn calls each at P={P} (f32 cache; {os.cpu_count()} host cores "
-                      f"present), {secs * 1e3:.0f} ms wall"}
+                      f"op_attn calls each at P={P} (C restatement, f32 cache; "
+                      f"{os.cpu_count()} host cores present), {secs * 1e3:.0f} ms wall"}
 
 
 def profiled_traffic():
