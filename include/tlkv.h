@@ -49,6 +49,7 @@ enum {
     TL_ERANGE    = -2,   /* slot or position outside the cache */
     TL_EHIP      = -3,   /* HIP runtime error */
     TL_ENOMEM    = -4,   /* device allocation failed */
+    TL_EBUSY     = -5,   /* a shared resource is in use by an overlapping call */
 };
 
 /* One layer of the KV cache (the device twin of AttnKvCache). */
@@ -195,8 +196,13 @@ int tl_attn(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
  * fixed region per GPU (32 MiB, held until the process ends; set up by
  * tl_init or the first call on a device).  Calls needing more than it holds
  * fail with TL_ERANGE (prefill batches take fewer key splits to fit).  All
- * calls on one GPU share the region: calls that overlap on one GPU (two
- * streams, two threads) race and must be serialised by the caller. */
+ * calls on one GPU share the region, so calls must not overlap on one GPU;
+ * the overlaps the library can see fail with TL_EBUSY instead of racing: a
+ * call while another thread's call is inside the function, and a call on
+ * another stream than the previous call's while that call's work has not
+ * finished.  Under HIP graph capture, call tl_init(device) first (setting the
+ * region up synchronises the device), and keep replays of captured calls
+ * from overlapping other calls: the library cannot see those. */
 int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void *stream);
 
 /* Attention only (no append): the rows at positions < pos+n are assumed

@@ -77,3 +77,40 @@ def test_noalloc_equals_attn_twice(T, kind):
         k0 = layers[0].k.cpu().numpy().view(np.uint16)
         k1 = layers[1].k.cpu().numpy().view(np.uint16)
         assert np.array_equal(k0, k1), f"call {i}: appended rows differ"
+
+
+def test_noalloc_refuses_overlap_on_another_stream(T):
+    """A call on another stream while the previous call's work is still
+    queued fails with TL_EBUSY instead of racing on the shared region; once
+    that work has finished the same call runs, and both calls match tl_attn
+    bit for bit (each appends the same row, then attends over the cache)."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos = 32, 8, 128, 4200, 4095
+    rng = np.random.default_rng(77)
+    kd = n_kv * hd
+    L = tlkv.Layer(cap, n_kv, hd)
+    hk = T.from_numpy(rng.standard_normal((pos, kd)).astype(np.float32)).cuda()
+    hv = T.from_numpy(rng.standard_normal((pos, kd)).astype(np.float32)).cuda()
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(hk), tlkv.ptr(hv), kd, None, 0, pos,
+                                       None))
+    q, k, v = (T.from_numpy(rng.standard_normal((1, w)).astype(np.float32)).cuda()
+               for w in (n_head * hd, kd, kd))
+    outs = [T.zeros((1, n_head * hd), dtype=T.float32, device="cuda") for _ in range(3)]
+    args = [tlkv.attn_args(q, k, v, o, None, pos, 1, n_head, hd, n_kv, 0, O.scale_of(hd))
+            for o in outs]
+    s1, s2 = T.cuda.Stream(), T.cuda.Stream()
+    T.cuda.synchronize()
+    lib = tlkv.lib()
+    big = T.randn((8192, 8192), device="cuda")
+    T.cuda.synchronize()
+    with T.cuda.stream(s1):                 # ~0.2 s of queued work on s1
+        for _ in range(20):
+            big = T.mm(big, big).clamp_(-1, 1)
+    assert lib.tl_attn_noalloc(L.desc, args[0], s1.cuda_stream) == tlkv.TL_OK
+    assert lib.tl_attn_noalloc(L.desc, args[1], s2.cuda_stream) == tlkv.TL_EBUSY
+    s1.synchronize()
+    assert lib.tl_attn_noalloc(L.desc, args[1], s2.cuda_stream) == tlkv.TL_OK
+    tlkv.check(lib.tl_attn(L.desc, args[2], s2.cuda_stream))
+    s2.synchronize()
+    a, b, c = (o.cpu().numpy().view(np.uint32) for o in outs)
+    assert np.array_equal(a, c) and np.array_equal(b, c)

@@ -37,6 +37,9 @@
  */
 #include "tl_decode_kernels.h"
 
+#include <atomic>
+#include <mutex>
+
 template <int D>
 static DecKernel pick_kernel(int G, bool rope, bool q8) {
     if (q8) return tl_pick_decode_q8(D, G, rope);   /* tl_decode_q8.hip */
@@ -60,28 +63,37 @@ static u32 tuned(int key, u32 dflt) {
     return v ? v : dflt;
 }
 
+/* CUs of the current device (cached per device; launches from several host
+ * threads may fill the cache at once and store the same value) */
 static int cu_count() {
-    static int cus[16] = {0};
+    static std::atomic<int> cus[16];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (!n) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
             n = 256;
-        cus[dev] = n;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return n;
 }
 
-/* resident workgroups per CU of a kernel (cached per entry point) */
+/* resident workgroups per CU of a kernel (cached per entry point, under a
+ * lock: several host threads may launch at once) */
 static int resident_per_cu(const void *fn, int threads) {
+    static std::mutex mu;
     static const void *keys[64];
     static int vals[64];
     static int n = 0;
-    for (int i = 0; i < n; i++)
-        if (keys[i] == fn) return vals[i];
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        for (int i = 0; i < n; i++)
+            if (keys[i] == fn) return vals[i];
+    }
     int b = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, threads, 0) != hipSuccess || b < 1) b = 1;
+    std::lock_guard<std::mutex> lk(mu);
     if (n < 64) {
         keys[n] = fn;
         vals[n++] = b;

@@ -51,33 +51,6 @@ TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
  * the level every XCD sees), the policy of agent-scope atomics. */
 #define TL_SC1 16
 
-/* Optional per-workgroup timeline (measurement builds only, -DTL_DEC_TRACE):
- * 16 u64 per workgroup: s_memrealtime (100 MHz) at launch entry (0),
- * stream start (1), stream end (2), partial written (3), merge end (4),
- * first tile in (5), epilogue LDS done (8), merge: counter seen (9),
- * partials loaded (10); the XCC (6) and HW (7) ids. */
-#ifdef TL_DEC_TRACE
-__device__ u64 tl_dec_trace[8192 * 16];
-#define TL_TRACE(i)                                                                    \
-    do {                                                                               \
-        if (threadIdx.x == 0 && blockIdx.x < 8192)                                     \
-            tl_dec_trace[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime();      \
-    } while (0)
-#define TL_TRACE_IDS()                                                                 \
-    do {                                                                               \
-        if (threadIdx.x == 0 && blockIdx.x < 8192) {                                   \
-            tl_dec_trace[blockIdx.x * 16 + 6] = __builtin_amdgcn_s_getreg((3 << 11) | 20); \
-            tl_dec_trace[blockIdx.x * 16 + 7] = __builtin_amdgcn_s_getreg((31 << 11) | 4); \
-        }                                                                              \
-    } while (0)
-extern "C" int tl_dec_trace_read(void *host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_dec_trace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#else
-#define TL_TRACE(i) do {} while (0)
-#define TL_TRACE_IDS() do {} while (0)
-#endif
-
 /* Split merge as its own launch (prefill key splits, and decode splits whose
  * partials exceed the in-launch merge).  D/4 threads per output row of one
  * head, each owning a float4: it folds the n_split partials of its float4
@@ -170,14 +143,6 @@ TL_DEV void lds_dma4(u32 m0, const void *base, u32 voff) {
 
 /* Q8_0 tiles: 6 loads each (K and V values 2 + 2, K and V scales 1 + 1) */
 TL_DEV void wait_tiles_q8(u32 n) {
-#ifdef TL_Q8_NOSCALE
-    switch (n) {
-    case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); return;
-    case 1: __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory"); return;
-    case 2: __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory"); return;
-    default: __asm__ volatile("s_waitcnt vmcnt(12)" ::: "memory"); return;
-    }
-#endif
     switch (n) {
     case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     case 1: __asm__ volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
@@ -473,7 +438,6 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
     }
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    TL_TRACE(10);
     for (int col = col0; col < COLS; col += NT / TPC) {
         const int h = col / (D / 4), d = (col % (D / 4)) * 4;
         const float2 *mlh = s_ml + (u32)h * ns;
@@ -614,8 +578,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    TL_TRACE(0);
-    TL_TRACE_IDS();
     /* this launch's epoch (dist merge) is the launch counter + 1: the
      * counter is read now (device-coherent, as the closers' increments are)
      * and first used at the end, so nothing waits for it here */
@@ -798,7 +760,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         }
     }
     __syncthreads();
-    TL_TRACE(1);
 
     const u16 *Kbase = sq.k + (u64)kvh * sq.cap * D;
     const u16 *Vbase = sq.v + (u64)kvh * sq.cap * D;
@@ -844,12 +805,10 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             const u32 sph = phys(min(tb + (u32)srow, klast));
             const u32 soff = (sph * (D / 32) + 2 * sw) * 2;
             const u32 ls = scl_lds + (j % S) * 256;
-#ifndef TL_Q8_NOSCALE
             if (lane < 32) {
                 lds_dma4(ls, KS, soff);
                 lds_dma4(ls + 128, VS, soff);
             }
-#endif
             return;
         }
 #pragma unroll
@@ -892,11 +851,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             wait_tiles_q8(after < (u32)(S - 1) ? after : (u32)(S - 1));
         else
             wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
-#ifdef TL_DEC_TRACE
-        if (j == 0 && lane == 0 && blockIdx.x < 8192)
-            tl_dec_trace[blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();
-#endif
-#ifndef TL_DEC_NOCOMPUTE
         const uint4 *st = &s_ring[wave][(j % S) * STAGE_U];
         if constexpr (Q8) {
             const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
@@ -905,7 +859,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         } else {
             ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
         }
-#endif
         if (j + S < nj) issue(j + S);
     }
     /* tiles with new rows: cache rows and staged new rows through registers */
@@ -1028,8 +981,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                             make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
                                         acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
         __syncthreads();
-        if (h0 == 0) TL_TRACE(2);
-        if (h0 == 0) TL_TRACE(8);
         const int h = h0 + rhh;
         if (rhh < HB && h < G) {
             const int d = rsub * 16 + rk4 * 4;
@@ -1111,10 +1062,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
      * the whole group. */
     __shared__ u32 s_last, s_flag;
     __shared__ u64 s_todo;
-    TL_TRACE(12);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    TL_TRACE(3);
     u32 *arrive = p.counters + grp * TL_MERGE_PAD;
     if (p.dist) {
         __shared__ u32 s_epoch;
@@ -1159,20 +1108,28 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         const bool closer = s_last == n_split - 1;
         if (!closer) {
             if (!s_flag || c0 >= c1) return;                 /* the last to arrive covers it */
-            TL_TRACE(9);
             /* claim the slice: from here this workgroup merges it unconditionally */
             if (tid == 0)
                 __hip_atomic_store(&tags[split], epoch, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
-            TL_TRACE(4);
             return;
         }
-        TL_TRACE(9);
         if (tid == 0) {
             __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(p.counters + TL_MERGE_LAUNCHES, 1u, __ATOMIC_RELAXED,
+            /* the last group of the launch to close advances the launch
+             * counter: by then every workgroup of the launch has arrived, so
+             * has read the counter, and all of them use the same epoch (a
+             * workgroup dispatched after an early group's close would
+             * otherwise see the next one and make its peers' polls time out) */
+            const u32 closed = __hip_atomic_fetch_add(p.counters + TL_MERGE_CLOSED, 1u,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (closed == n_groups - 1) {
+                __hip_atomic_store(p.counters + TL_MERGE_CLOSED, 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(p.counters + TL_MERGE_LAUNCHES, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
         /* slices whose owner has not claimed them (yet) */
@@ -1193,7 +1150,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         __syncthreads();
         for (u64 todo = s_todo; todo; todo &= todo - 1)
             merge_slice<D, G, W>(p, pb, r, kvh, sq, (u32)__builtin_ctzll(todo), cps);
-        TL_TRACE(4);
         return;
     }
     if (tid == 0)
@@ -1203,13 +1159,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     if (closer && tid == 0)
         __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!closer) return;
-    TL_TRACE(9);
     /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */
     split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0]);
-#ifdef TL_DEC_TRACE
-    __syncthreads();
-    TL_TRACE(4);
-#endif
 }
 
 /* One decode kernel instance: entry point, K (or V) bytes per wave tile and

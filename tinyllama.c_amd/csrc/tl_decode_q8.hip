@@ -1,10 +1,8 @@
 /*
  * tl_decode_q8.hip — the Q8_0-cache instances of attn_decode_ring_kernel
  * (tl_decode_kernels.h; design in tl_decode.hip), in their own translation
- * unit so the kernel instances build in parallel.  Measurement-trace builds
- * instrument only the f16 instances.
+ * unit so the kernel instances build in parallel.
  */
-#undef TL_DEC_TRACE
 #include "tl_decode_kernels.h"
 
 template <int D>

@@ -75,6 +75,10 @@ struct DecParams {
 #define TL_MERGE_MAX_SPLIT_DIST 64
 #define TL_MERGE_TAGS (TL_MERGE_MAX_GROUPS * TL_MERGE_PAD)
 #define TL_MERGE_LAUNCHES (TL_MERGE_TAGS + TL_MERGE_MAX_SPLIT_DIST * TL_MERGE_MAX_GROUPS)
+/* groups of the current launch whose closer has run (dist merge): the last
+ * one resets it and advances TL_MERGE_LAUNCHES, so the launch counter moves
+ * once per launch, after every workgroup of the launch has read it */
+#define TL_MERGE_CLOSED (TL_MERGE_LAUNCHES + TL_MERGE_PAD / 2)
 #define TL_MERGE_CNT_WORDS (TL_MERGE_LAUNCHES + TL_MERGE_PAD)
 
 /* Chunked-prefill launch (one OP_ATTN batch of one session). */

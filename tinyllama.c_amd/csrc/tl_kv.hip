@@ -743,6 +743,14 @@ extern "C" int tl_attn_noappend(const tl_kv_layer *L, const tl_attn_args *a, voi
     return attn_core(L, a, false, rc0, (hipStream_t)stream);
 }
 
+/* Guards of the fixed region: one call inside tl_attn_noalloc per device at
+ * a time, and the stream and completion event of the last uncaptured call,
+ * so that a call on another stream while that one's work is still queued or
+ * running is refused instead of racing on the region. */
+static std::atomic<int> g_scratch_busy[TL_MAX_DEV];
+static hipStream_t g_scratch_last[TL_MAX_DEV];
+static hipEvent_t g_scratch_done[TL_MAX_DEV];
+
 extern "C" int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void *stream) {
     int rc = check_args(L, a);
     if (rc) return rc;
@@ -750,13 +758,47 @@ extern "C" int tl_attn_noalloc(const tl_kv_layer *L, const tl_attn_args *a, void
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= TL_MAX_DEV) return tl_fail(TL_EINVAL, "device %d", dev);
-    TlWorkspace *w;
-    rc = scratch_setup(dev, &w);
-    if (rc) return rc;
-    TlWsFixed scope(w);
-    RopeCfg rc0;
-    rope_cfg(L, nullptr, rc0);
-    return attn_core(L, a, true, rc0, (hipStream_t)stream);
+    const hipStream_t st = (hipStream_t)stream;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(st, &cs));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    int idle = 0;
+    if (!g_scratch_busy[dev].compare_exchange_strong(idle, 1, std::memory_order_acquire))
+        return tl_fail(TL_EBUSY, "noalloc: another call on device %d is in progress", dev);
+    struct Release {
+        int d;
+        ~Release() { g_scratch_busy[d].store(0, std::memory_order_release); }
+    } release{dev};
+    TlWorkspace *w = &g_scratch_ws[dev];
+    if (!w->acc) {
+        if (capturing)
+            return tl_fail(TL_EINVAL, "noalloc: call tl_init(%d) before capturing", dev);
+        rc = scratch_setup(dev, &w);
+        if (rc) return rc;
+    }
+    hipEvent_t &done = g_scratch_done[dev];
+    if (!capturing) {
+        if (!done) HIP_TRY(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+        else if (g_scratch_last[dev] != st) {
+            const hipError_t q = hipEventQuery(done);
+            if (q == hipErrorNotReady)
+                return tl_fail(TL_EBUSY,
+                               "noalloc: the previous call's work on another stream has not "
+                               "finished");
+            if (q != hipSuccess) HIP_TRY(q);
+        }
+    }
+    {
+        TlWsFixed scope(w);
+        RopeCfg rc0;
+        rope_cfg(L, nullptr, rc0);
+        rc = attn_core(L, a, true, rc0, st);
+    }
+    if (!rc && !capturing) {
+        HIP_TRY(hipEventRecord(done, st));
+        g_scratch_last[dev] = st;
+    }
+    return rc;
 }
 
 static int decode_batch(const tl_decode_seq *seqs, uint32_t n_seq, uint32_t n_head,

@@ -56,6 +56,10 @@ class TlError(RuntimeError):
     pass
 
 
+# return codes (include/tlkv.h)
+TL_OK, TL_EINVAL, TL_ERANGE, TL_EHIP, TL_ENOMEM, TL_EBUSY = 0, -1, -2, -3, -4, -5
+
+
 # launch-shape overrides (include/tlkv.h TL_TUNE_*)
 TUNE_DECODE_WGS, TUNE_DECODE_MIN_KEYS, TUNE_DECODE_MERGE_KERNEL = 0, 1, 2
 TUNE_PREFILL_SPLITS, TUNE_NO_PREFILL, TUNE_DECODE_SINGLE_MERGE = 3, 4, 5
