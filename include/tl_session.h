@@ -130,7 +130,9 @@ const uint32_t    *tl_session_device_slots(const tl_session *s);  /* device [ctx
  * has not seen), in `stream` order, and returns the device table in
  * *d_slots.  It consumes the cache's change mark (tl_kv_cache_take_dirty), so
  * one cache feeds one mirror.  Fails with TL_ERANGE for a slot outside the
- * mirror's ctx_size. */
+ * mirror's ctx_size.  A sync that uploads on another stream than the
+ * previous upload first synchronises that stream (its queued copies and
+ * readers of the map must finish before the map is overwritten). */
 typedef struct tl_slot_mirror tl_slot_mirror;
 int  tl_slot_mirror_create(uint32_t ctx_size, tl_slot_mirror **out);
 void tl_slot_mirror_destroy(tl_slot_mirror *m);

@@ -516,6 +516,8 @@ struct tl_slot_mirror {
     uint32_t     *stage;       /* pinned [STAGE_WORDS] */
     uint32_t      stage_pos;
     KvRadixCache *seen;        /* the cache whose change marks the mirror follows */
+    void         *last;        /* stream of the last sync that queued work */
+    int           queued;      /* some sync has queued work on `last` */
 };
 
 int tl_slot_mirror_create(uint32_t ctx_size, tl_slot_mirror **out) {
@@ -562,6 +564,19 @@ int tl_slot_mirror_sync(tl_slot_mirror *m, KvRadixCache *radix, void *stream,
                 m->seen = NULL;   /* re-upload everything next time */
                 return fail(TL_ERANGE, "slot mirror: slot outside the cache");
             }
+        /* A sync on another stream than the last one: the copies (and the
+         * kernels reading the mirror) queued there may still read the staged
+         * words and the device map this upload overwrites, so let them
+         * finish first; uploads on one stream are ordered by the stream. */
+        if (m->queued && m->last != stream) {
+            if (hipStreamSynchronize((hipStream_t)m->last) != hipSuccess) {
+                m->seen = NULL;
+                return fail(TL_EHIP, "slot mirror: sync of the previous stream");
+            }
+            m->queued = 0;
+        }
+        m->last = stream;
+        m->queued = 1;
         int rc = stage_upload(m->stage, &m->stage_pos, (hipStream_t)stream, m->d_slots + lo,
                               req->slots + lo, len - lo);
         if (rc) {
