@@ -85,6 +85,7 @@ static int ws_grow(TlWorkspace *w, size_t acc_floats, size_t ml_pairs, size_t co
         size_t cap = acc_floats + acc_floats / 4 + 1024;
         if (hipMalloc((void **)&w->acc, cap * sizeof(float)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu floats", cap);
+        HIP_TRY(hipMemset(w->acc, 0, cap * sizeof(float)));
         w->acc_cap = cap;
     }
     if (ml_pairs > w->ml_cap) {
@@ -94,6 +95,11 @@ static int ws_grow(TlWorkspace *w, size_t acc_floats, size_t ml_pairs, size_t co
         size_t cap = ml_pairs + ml_pairs / 4 + 256;
         if (hipMalloc((void **)&w->ml, cap * sizeof(float2)) != hipSuccess)
             return tl_fail(TL_ENOMEM, "workspace: %zu pairs", cap);
+        /* zero: the in-launch merge reads epoch-tagged records here, which
+         * must not match by chance what an earlier owner of the memory (a
+         * workspace of another stream, with its own launch counter) left */
+        HIP_TRY(hipMemset(w->ml, 0, cap * sizeof(float2)));
+        HIP_TRY(hipDeviceSynchronize());
         w->ml_cap = cap;
     }
     if (counters > w->cnt_cap) {
@@ -180,7 +186,7 @@ static int scratch_setup(int dev, TlWorkspace **out) {
         unsigned char *base = (unsigned char *)ptr;
         u32 *cnt = (u32 *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4 +
                            (size_t)TL_SCRATCH_ML_PAIRS * 8);
-        HIP_TRY(hipMemset(cnt, 0, (size_t)TL_SCRATCH_COUNTERS * 4));
+        HIP_TRY(hipMemset(base, 0, TL_SCRATCH_BYTES));
         HIP_TRY(hipDeviceSynchronize());
         w->acc = (float *)base;
         w->ml = (float *)(base + (size_t)TL_SCRATCH_ACC_FLOATS * 4);
