@@ -678,6 +678,46 @@ def run_state_snapshot(torch, tlkv, lib, sh):
     return out
 
 
+DECODE_KERNEL = "attn_decode_ring_kernel<128, 4, false, false>"
+
+
+def split_trace(path, warmup, steps):
+    """The config-4 decode launches of a profiled run, by variant: they are
+    the first dispatches of DECODE_KERNEL, in the order main() issues them —
+    (warmup + steps) x 32 OP_ATTN launches (identity slot table, fused
+    append), then 32 + min(128, steps) x 32 over the contiguous cache
+    (without the slot table or append), then 32 + min(128, steps) x 32
+    through the permuted slot table; the first 32 of the last two are
+    untimed warm-ups.  Prints one markdown table of average durations."""
+    import csv
+    L = CFG4["L"]
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r.get("Kernel_Name", "")
+            if DECODE_KERNEL.replace(" ", "") in name.replace(" ", ""):
+                rows.append((int(r["Dispatch_Id"]), int(r["Start_Timestamp"]),
+                             int(r["End_Timestamp"])))
+    rows.sort()
+    n_main, n_side = (warmup + steps) * L, min(128, steps) * L
+    phases = [("identity slot table + fused append (the timed `value` loop)", warmup * L,
+               n_main),
+              ("contiguous cache, no append (decode_contiguous)", n_main + L, n_main + L + n_side),
+              ("permuted slot table, no append (decode_permuted_slots)", n_main + 2 * L + n_side,
+               n_main + 2 * L + 2 * n_side)]
+    print("| variant | launches | avg us | min us | max us | avg start-to-start us |")
+    print("|---|---|---|---|---|---|")
+    for nm, a, b in phases:
+        seg = rows[a:b]
+        if not seg:
+            continue
+        d = np.array([(e - s_) / 1e3 for _, s_, e in seg])
+        st = np.array([s_ for _, s_, _ in seg], dtype=np.float64)
+        gap = np.diff(st).mean() / 1e3 if len(st) > 1 else float("nan")
+        print(f"| {nm} | {len(seg)} | {d.mean():.2f} | {d.min():.2f} | {d.max():.2f} | "
+              f"{gap:.2f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -692,7 +732,13 @@ def main():
     ap.add_argument("--ctx", type=int, default=CFG4["ctx"])
     ap.add_argument("--configs", default="1,2,3,5",
                     help="other BASELINE configs to measure after the north star ('' = none)")
+    ap.add_argument("--split-trace", metavar="CSV",
+                    help="no run: split a rocprofv3 kernel-trace CSV of a run with the same "
+                         "--steps/--warmup into the config-4 decode variants, print markdown")
     args = ap.parse_args()
+    if args.split_trace:
+        split_trace(args.split_trace, args.warmup, args.steps)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; runs on several GPUs "
                                    "are not part of it"}))

@@ -181,10 +181,18 @@ int tl_launch_merge(const DecParams &p, u32 n_rows_total, u32 head_dim, hipStrea
     if (p.n_split > TL_MERGE_MAX_SPLIT) return tl_fail(TL_EINVAL, "merge: %u splits", p.n_split);
     const u32 n_out = n_rows_total * p.n_head;
     const dim3 mg((u32)(((u64)n_out * (head_dim / 4) + 255) / 256));
+    MergeParams m;
+    for (u32 i = 0; i < TL_MAX_BATCH_SEQ; i++) m.dst[i] = p.seq[i].dst;
+    m.rows_per_seq = p.rows_per_seq;
+    m.n_head = p.n_head;
+    m.q_stride = p.q_stride;
+    m.n_split = p.n_split;
+    m.ws_acc = p.ws_acc;
+    m.ws_ml = p.ws_ml;
     switch (head_dim) {
-    case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(256), 0, st, p, n_out); break;
-    case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(256), 0, st, p, n_out); break;
-    case 256: hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(256), 0, st, p, n_out); break;
+    case 64: hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(256), 0, st, m, n_out); break;
+    case 128: hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(256), 0, st, m, n_out); break;
+    case 256: hipLaunchKernelGGL(attn_merge_kernel<256>, mg, dim3(256), 0, st, m, n_out); break;
     default: return tl_fail(TL_EINVAL, "merge: head_dim %u", head_dim);
     }
     HIP_TRY(hipGetLastError());

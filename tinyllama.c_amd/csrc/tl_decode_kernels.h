@@ -58,8 +58,16 @@ TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
  * together): out = sum_s exp2(m_s - M) acc_s / sum_s exp2(m_s - M) l_s.
  * grid = ceil(rows * n_head * D/4 / 256), no LDS, no barriers. */
 #define TL_MERGE_MAX_SPLIT 1024
+/* the merge's arguments: a small block (the kernel arguments are copied per
+ * launch, and a chunked prefill runs one merge per layer and chunk) */
+struct MergeParams {
+    float *dst[TL_MAX_BATCH_SEQ];
+    uint32_t rows_per_seq, n_head, q_stride, n_split;
+    const float *ws_acc;
+    const float2 *ws_ml;
+};
 template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p, u32 n_out) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(const MergeParams p, u32 n_out) {
     constexpr float NEG_INF = -__builtin_huge_valf();
     constexpr int C4 = D / 4;
     constexpr int K = 8;
@@ -106,7 +114,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const DecParams p, u32 
         }
     }
     const float inv = 1.0f / L;
-    *(float4 *)&p.seq[si].dst[(u64)r * p.q_stride + (u64)hq * D + d] =
+    *(float4 *)&p.dst[si][(u64)r * p.q_stride + (u64)hq * D + d] =
         make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
 }
 

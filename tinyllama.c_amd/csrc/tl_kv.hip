@@ -323,8 +323,8 @@ TL_DEV uint4 cvt8(const float *src) {
 
 /* grid: (blocks, n_seg).  One thread per 8-element vector of one row of one
  * head; consecutive threads cover consecutive 16-byte pieces of a row. */
-template <bool ROPE>
-__global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
+template <bool ROPE, int NS>
+__global__ __launch_bounds__(256) void kv_append_kernel(const AppendParamsN<NS> p) {
     const AppendSeg &sg = p.seg[blockIdx.y];
     const u32 vpr = sg.head_dim >> 3;
     const u64 total = (u64)sg.n * sg.n_kv * vpr;
@@ -356,12 +356,23 @@ int tl_launch_append(const AppendParams &p, u32 n_seg, hipStream_t stream) {
     if (most == 0) return TL_OK;
     u64 blocks = (most + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    if (p.rope.rdim)
-        hipLaunchKernelGGL(kv_append_kernel<true>, dim3((u32)blocks, n_seg), dim3(256), 0,
-                           stream, p);
-    else
-        hipLaunchKernelGGL(kv_append_kernel<false>, dim3((u32)blocks, n_seg), dim3(256), 0,
-                           stream, p);
+    if (n_seg == 1) {
+        AppendParamsN<1> p1;
+        p1.seg[0] = p.seg[0];
+        p1.rope = p.rope;
+        if (p.rope.rdim)
+            hipLaunchKernelGGL((kv_append_kernel<true, 1>), dim3((u32)blocks, 1), dim3(256), 0,
+                               stream, p1);
+        else
+            hipLaunchKernelGGL((kv_append_kernel<false, 1>), dim3((u32)blocks, 1), dim3(256), 0,
+                               stream, p1);
+    } else if (p.rope.rdim) {
+        hipLaunchKernelGGL((kv_append_kernel<true, TL_MAX_BATCH_SEQ>), dim3((u32)blocks, n_seg),
+                           dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((kv_append_kernel<false, TL_MAX_BATCH_SEQ>), dim3((u32)blocks, n_seg),
+                           dim3(256), 0, stream, p);
+    }
     HIP_TRY(hipGetLastError());
     return TL_OK;
 }

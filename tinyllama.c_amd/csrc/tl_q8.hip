@@ -116,10 +116,12 @@ struct Q8AppendSeg {
     const u32 *slots;
     u32 cap, ring, n_kv, head_dim, kv_stride, pos, n;
 };
-struct Q8AppendParams {
-    Q8AppendSeg seg[TL_MAX_BATCH_SEQ];
+template <int NS>
+struct Q8AppendParamsN {
+    Q8AppendSeg seg[NS];
     RopeCfg rope;            /* applied to K before quantizing (rdim 0: none) */
 };
+typedef Q8AppendParamsN<TL_MAX_BATCH_SEQ> Q8AppendParams;
 
 /* 8 values of a block whose scale is 1/id -> 8 int8 in two words */
 TL_DEV uint2 q8_pack8(const float (&x)[8], float id) {
@@ -146,8 +148,8 @@ TL_DEV float amax8(const float (&x)[8]) {
  * plain append); the 4 lanes of a block are an aligned group of a wave
  * (grid stride and row length are multiples of 4), so the block max is a
  * DPP max within the group. */
-template <bool ROPE>
-__global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParams pp) {
+template <bool ROPE, int NS>
+__global__ __launch_bounds__(256) void kv_append_q8_kernel(const Q8AppendParamsN<NS> pp) {
     const Q8AppendSeg &p = pp.seg[blockIdx.y];
     const u32 opr = p.head_dim >> 3;
     const u64 total = (u64)p.n * p.n_kv * opr;
@@ -224,10 +226,21 @@ static int launch_append_q8(const Q8AppendParams &p, u32 n_seg, hipStream_t st) 
     if (most == 0) return TL_OK;
     u64 blocks = (most + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    if (p.rope.rdim)
-        hipLaunchKernelGGL(kv_append_q8_kernel<true>, dim3((u32)blocks, n_seg), dim3(256), 0, st, p);
-    else
-        hipLaunchKernelGGL(kv_append_q8_kernel<false>, dim3((u32)blocks, n_seg), dim3(256), 0, st, p);
+    if (n_seg == 1) {   /* one segment's arguments: a smaller per-launch copy */
+        Q8AppendParamsN<1> p1;
+        p1.seg[0] = p.seg[0];
+        p1.rope = p.rope;
+        if (p.rope.rdim)
+            hipLaunchKernelGGL((kv_append_q8_kernel<true, 1>), dim3((u32)blocks, 1), dim3(256), 0, st, p1);
+        else
+            hipLaunchKernelGGL((kv_append_q8_kernel<false, 1>), dim3((u32)blocks, 1), dim3(256), 0, st, p1);
+    } else if (p.rope.rdim) {
+        hipLaunchKernelGGL((kv_append_q8_kernel<true, TL_MAX_BATCH_SEQ>), dim3((u32)blocks, n_seg),
+                           dim3(256), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((kv_append_q8_kernel<false, TL_MAX_BATCH_SEQ>), dim3((u32)blocks, n_seg),
+                           dim3(256), 0, st, p);
+    }
     HIP_TRY(hipGetLastError());
     return TL_OK;
 }
