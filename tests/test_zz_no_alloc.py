@@ -4,7 +4,10 @@ same inputs, through the C ABI: calls in a row, each followed by a smaller
 one, so the second reads a region the first left behind.  Decode outputs are
 bit-identical (same kernels, same split count); prefill batches may take
 fewer key splits to fit the region, so they agree within 1e-4 and both stay
-within 2e-3 of the oracle.  The appended cache rows are identical."""
+within 2e-3 of the oracle.  The appended cache rows are identical.  Also:
+overlapping calls the library can see are refused with TL_EBUSY; the call
+captured in a HIP graph replays bit-identically to the eager call; a first
+call under capture before tl_init is refused with TL_EINVAL."""
 import numpy as np
 import pytest
 
@@ -114,3 +117,76 @@ def test_noalloc_refuses_overlap_on_another_stream(T):
     s2.synchronize()
     a, b, c = (o.cpu().numpy().view(np.uint32) for o in outs)
     assert np.array_equal(a, c) and np.array_equal(b, c)
+
+
+def test_noalloc_graph_replay(T):
+    """The use case: tl_attn_noalloc captured in a HIP graph (after tl_init)
+    and replayed, with new q written eagerly between replays; every replay
+    equals the eager no-allocation call on the same inputs bit for bit and
+    the oracle within tolerance."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos = 32, 8, 128, 8400, 8191
+    rng = np.random.default_rng(2025)
+    kd, qd = n_kv * hd, n_head * hd
+    hk = rng.standard_normal((pos + 1, kd)).astype(np.float32)
+    hv = rng.standard_normal((pos + 1, kd)).astype(np.float32)
+    L = tlkv.Layer(cap, n_kv, hd)
+    dhk, dhv = T.from_numpy(hk[:pos]).cuda(), T.from_numpy(hv[:pos]).cuda()
+    tlkv.check(tlkv.lib().tl_kv_append(L.desc, tlkv.ptr(dhk), tlkv.ptr(dhv), kd, None, 0, pos,
+                                       None))
+    T.cuda.synchronize()
+    C = O.Cache(cap, n_kv, hd)
+    C.append(hk[:pos], hv[:pos], None, 0, pos)
+    dq = T.zeros((1, qd), dtype=T.float32, device="cuda")
+    dk = T.from_numpy(hk[pos:]).cuda()
+    dv = T.from_numpy(hv[pos:]).cuda()
+    out = T.zeros((1, qd), dtype=T.float32, device="cuda")
+    a = tlkv.attn_args(dq, dk, dv, out, None, pos, 1, n_head, hd, n_kv, 0, O.scale_of(hd))
+    lib = tlkv.lib()
+    s = T.cuda.Stream()
+    T.cuda.synchronize()
+    g = T.cuda.CUDAGraph()
+    with T.cuda.graph(g, stream=s):
+        tlkv.check(lib.tl_attn_noalloc(L.desc, a, s.cuda_stream))
+    for i in range(4):
+        q = rng.standard_normal((1, qd)).astype(np.float32)
+        dq.copy_(T.from_numpy(q))
+        T.cuda.synchronize()
+        g.replay()
+        T.cuda.synchronize()
+        got = out.cpu().numpy().copy()
+        out.zero_()
+        tlkv.check(lib.tl_attn_noalloc(L.desc, a, s.cuda_stream))
+        s.synchronize()
+        assert np.array_equal(got.view(np.uint32), out.cpu().numpy().view(np.uint32)), i
+        ref = O.attn(C, q, hk[pos:], hv[pos:], None, pos, 1, n_head)
+        assert np.abs(got - ref).max() < TOL, i
+
+
+def test_noalloc_capture_before_init_is_refused():
+    """In a process that has not called tl_init, a first tl_attn_noalloc under
+    graph capture fails with TL_EINVAL (its one-time set-up would synchronise
+    the device) instead of breaking the capture.  Run in a child process: this
+    one has set the region up already."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    pkg = os.path.join(os.path.dirname(here), "tinyllama.c_amd")
+    code = f"""
+import sys
+sys.path.insert(0, {pkg!r})
+import torch, tlkv
+L = tlkv.Layer(1024, 8, 128)
+q = torch.zeros((1, 4096), device="cuda"); k = torch.zeros((1, 1024), device="cuda")
+out = torch.zeros((1, 4096), device="cuda")
+a = tlkv.attn_args(q, k, k, out, None, 100, 1, 32, 128, 8, 0, 0.088)
+s = torch.cuda.Stream(); torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    rc = tlkv.lib().tl_attn_noalloc(L.desc, a, s.cuda_stream)
+print("rc", rc, flush=True)
+"""
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "rc -1" in r.stdout, r.stdout + r.stderr[-2000:]
