@@ -527,6 +527,50 @@ def run_config3(torch, tlkv, lib, sh, gen):
                     "planning) between launches; bytes are algorithmic"}
 
 
+def run_prefill_fused(torch, tlkv, lib, sh, gen, c, layers, slots, pf_ms, app_ms, pf_flops):
+    """The 64 config-4 chunks again (fresh rows, after the decode rows are
+    measured), as the executor issues them: one OP_ATTN per layer and chunk
+    (tl_attn: the prefill launch writes the chunk's rows itself), against
+    the separate tl_kv_append + tl_attn_noappend launches of phases 1-2.
+    The append's cost inside the fused launch is the fused time minus the
+    attention-only time of phase 2 (a difference of two timings)."""
+    L, Hq, Hkv, d, ub = c["L"], c["Hq"], c["Hkv"], c["d"], c["ub"]
+    kd, qd = Hkv * d, Hq * d
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    stream = torch.cuda.current_stream()
+    n_chunks = c["ctx"] // ub
+    ck = torch.empty((L, ub, kd), dtype=torch.float32, device="cuda")
+    cv = torch.empty((L, ub, kd), dtype=torch.float32, device="cuda")
+    cq = torch.empty((L, ub, qd), dtype=torch.float32, device="cuda")
+    co = torch.empty((L, ub, qd), dtype=torch.float32, device="cuda")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ms = 0.0
+    for ci in range(n_chunks):
+        p0 = ci * ub
+        ck.normal_(generator=gen)
+        cv.normal_(generator=gen)
+        cq.normal_(generator=gen)
+        e0.record(stream)
+        for l in range(L):
+            a = tlkv.attn_args(cq[l], ck[l], cv[l], co[l], slots, p0, ub, Hq, d, Hkv, 0, scale)
+            tlkv.check(lib.tl_attn(layers[l].desc, a, sh))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms += e0.elapsed_time(e1)
+    tokens = n_chunks * ub
+    extra = ms - pf_ms
+    return {"ms": round(ms, 2), "TFLOPs": round(pf_flops / (ms / 1e3) / 1e12, 2),
+            "separate_ms": round(pf_ms + app_ms, 2),
+            "append_extra_ms": round(extra, 2),
+            "append_tok_s": round(tokens / (extra / 1e3), 1) if extra > 0.05 * pf_ms else None,
+            "note": "OP_ATTN per layer and chunk with the append inside the prefill launch "
+                    "(no kv_append_kernel launches) vs append + attention launches "
+                    "(separate_ms = append.ms + prefill.ms); append_extra_ms = ms - prefill.ms, "
+                    "the append's cost inside the fused launch; append_tok_s = chunk tokens / "
+                    "append_extra_ms, reported only when that difference is above 5% of "
+                    "prefill.ms (below it is run-to-run noise)"}
+
+
 def run_q8(torch, tlkv, lib, sh, gen, c, steps):
     """Config 4 over a Q8_0 cache: the same 64 x 512-row chunks quantized into
     every layer (tl_kv_append_q8) with chunked-prefill attention over them
@@ -1001,6 +1045,8 @@ def main():
                           "frac_of_measured_mfma_ceiling": round(tf / mfma_ceil, 4),
                           "ms": round(pf_ms, 2), "flops": pf_flops,
                           "kernel": "attn_prefill_kernel<128,4> (+ split merge)"}
+        res["prefill_fused_append"] = run_prefill_fused(torch, tlkv, lib, sh, gen, c, layers,
+                                                        slots, pf_ms, app_ms, pf_flops)
     del layers, slots, q, k, v, out
     torch.cuda.empty_cache()
     if not args.no_q8:

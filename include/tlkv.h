@@ -123,7 +123,9 @@ int tl_init(int device);
 #define TL_TUNE_NO_PREFILL          4   /* 1: run every batch on the decode kernel */
 #define TL_TUNE_DECODE_SINGLE_MERGE 5   /* 1: the last split of a group merges all of it */
 #define TL_TUNE_DECODE_MERGE_POLLS  6   /* n: at most n - 1 polls per wait of the split merge */
-#define TL_TUNE_COUNT               7
+#define TL_TUNE_PREFILL_APPEND_POLLS 7  /* n: at most n - 1 polls per wait for the fused append */
+#define TL_TUNE_PREFILL_SEPARATE_APPEND 8 /* 1: prefill batches append in a launch of their own */
+#define TL_TUNE_COUNT               9
 int tl_set_tuning(int key, uint32_t value);
 uint32_t tl_get_tuning(int key);
 

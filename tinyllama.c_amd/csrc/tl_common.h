@@ -82,6 +82,28 @@ TL_DEV float group_max(float x) {
     return x;
 }
 
+/* 8 f32 -> 8 binary16 (RNE, NaN pinned), the append conversion */
+TL_DEV uint4 cvt8_f16_regs(float4 a, float4 b) {
+    return make_uint4(pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
+                      pack_f16x2(b.z, b.w));
+}
+TL_DEV uint4 cvt8_f16(const float *src) {
+    return cvt8_f16_regs(*(const float4 *)src, *(const float4 *)(src + 4));
+}
+/* the buffer builtins take and return GCC vectors; read their elements with
+ * v[i] into scalars (this compiler mis-reads __builtin_bit_cast of a vector
+ * element) */
+typedef u32 u32x4v_t __attribute__((vector_size(16)));
+typedef u32 u32x2v_t __attribute__((vector_size(8)));
+
+/* Raw buffer resource over `base` (offsets are bytes from base). */
+TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7ffffff0, 0x00020000);
+}
+/* Cache policy sc1: device-coherent access (written through to / read from
+ * the level every XCD sees), the policy of agent-scope atomics. */
+#define TL_SC1 16
+
 /* ---- RoPE (reference: src/backend/cpu/cpu_op.c:637-700) -------------------
  * Pair i of a head row rotates by angle pos * theta_i, theta_i =
  * 1 / powf(base, 2i / rdim).  NORM pairs elements (2i, 2i+1), NEOX pairs

@@ -15,14 +15,6 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 TL_DEV half2_t as_h2(u32 w) { return __builtin_bit_cast(half2_t, w); }
 
-/* 8 f32 -> 8 binary16 (RNE, NaN pinned), the append conversion */
-TL_DEV uint4 cvt8_f16_regs(float4 a, float4 b) {
-    return make_uint4(pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
-                      pack_f16x2(b.z, b.w));
-}
-TL_DEV uint4 cvt8_f16(const float *src) {
-    return cvt8_f16_regs(*(const float4 *)src, *(const float4 *)(src + 4));
-}
 
 TL_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -37,19 +29,6 @@ TL_DEV uint4 ld_stream(const u16 *ptr) {
 TL_DEV u32 perm_lo(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 TL_DEV u32 perm_hi(u32 a, u32 b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
-/* the buffer builtins take and return GCC vectors; read their elements with
- * v[i] into scalars (this compiler mis-reads __builtin_bit_cast of a vector
- * element) */
-typedef u32 u32x4v_t __attribute__((vector_size(16)));
-typedef u32 u32x2v_t __attribute__((vector_size(8)));
-
-/* Raw buffer resource over `base` (offsets are bytes from base). */
-TL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7ffffff0, 0x00020000);
-}
-/* Cache policy sc1: device-coherent access (written through to / read from
- * the level every XCD sees), the policy of agent-scope atomics. */
-#define TL_SC1 16
 
 /* Split merge as its own launch (prefill key splits, and decode splits whose
  * partials exceed the in-launch merge).  D/4 threads per output row of one
@@ -500,9 +479,7 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
  * words, each a memory round trip): a split that waits longer gives up, and
  * the last split to arrive merges what nobody else claimed. */
 #define TL_MERGE_SPIN 64
-#ifndef TL_MERGE_BACKOFF
 #define TL_MERGE_BACKOFF 4   /* s_sleep units (64 clocks) between polls */
-#endif
 
 /* Merge one slice of a group's output: columns [slice*cps, slice*cps + cps)
  * of the G*D/4 float4 columns (head, 4 dims).  One wave per column, lane s
@@ -557,9 +534,6 @@ TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq
  * appended by this launch (the last tiles of the last split) are filled
  * from registers after the ring has drained. */
 #define TL_RING_WAVES 8
-#ifndef TL_XCD_ROT
-#define TL_XCD_ROT 0
-#endif
 #define TL_RING_STAGES 2
 template <int D, int G, bool ROPE, bool Q8>
 __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
@@ -599,7 +573,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     u32 grp, split;
     if ((n_groups & 7) == 0) {
         const u32 xcd = bid & 7, local = bid >> 3;
-        grp = ((xcd + TL_XCD_ROT) & 7) + 8 * (local / n_split);
+        grp = xcd + 8 * (local / n_split);
         split = local % n_split;
     } else {
         grp = bid / n_split;

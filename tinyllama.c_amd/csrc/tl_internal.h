@@ -99,8 +99,19 @@ struct PrefParams {
     uint32_t n_split;
     float *ws_acc;
     float2 *ws_ml;
-    RopeCfg rope;            /* applied to q rows */
+    RopeCfg rope;            /* applied to q rows (and to appended K rows) */
+    /* fused append (f16 cache; kin NULL: none): the batch's K/V rows, f32
+     * [n][kv_stride], converted and written by the launch's own workgroups
+     * in units of 16 rows of one kv-head; flags[kvh * units + u] = epoch once
+     * a unit is in the cache; ctr[0] = launch counter (epoch - 1), ctr[1] =
+     * workgroups finished in this launch */
+    const float *kin, *vin;
+    uint32_t kv_stride, polls;
+    uint32_t *flags, *ctr;
 };
+/* the fused append's counters sit past the decode merge's in a workspace */
+#define TL_PF_CTR_WORDS 64
+#define TL_PF_ROWS 16
 
 struct TlWorkspace {
     float *acc;
@@ -158,4 +169,4 @@ int tl_launch_merge(const DecParams &p, uint32_t n_rows_total, uint32_t head_dim
 /* MFMA chunked-prefill attention (tl_prefill.hip). */
 bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a);
 int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &rope,
-                      hipStream_t st);
+                      hipStream_t st, bool append = false);

@@ -219,7 +219,8 @@ static std::once_flag g_tune_once;
 static void tune_seed() {
     static const char *const names[TL_TUNE_COUNT] = {
         "TL_DECODE_WGS", "TL_DECODE_MIN_KEYS", "TL_DECODE_MERGE_KERNEL", "TL_PREFILL_SPLITS",
-        "TL_NO_PREFILL", "TL_DECODE_SINGLE_MERGE", "TL_DECODE_MERGE_POLLS"};
+        "TL_NO_PREFILL", "TL_DECODE_SINGLE_MERGE", "TL_DECODE_MERGE_POLLS",
+        "TL_PREFILL_APPEND_POLLS", "TL_PREFILL_SEPARATE_APPEND"};
     for (int i = 0; i < TL_TUNE_COUNT; i++) {
         const char *e = getenv(names[i]);
         g_tune[i].store(e && *e ? (u32)strtoul(e, NULL, 10) : 0u, std::memory_order_relaxed);
@@ -681,16 +682,23 @@ static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
                      const RopeCfg &rope, hipStream_t st) {
     const LayerView lv = tl_view(L);
     if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(lv, a)) {
+        bool fused = false;
         if (append) {
             AppendParams ap;
             memset(&ap, 0, sizeof(ap));
             int rc = fill_seg(ap.seg[0], L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
             if (rc) return rc;
-            ap.rope = rope;
-            rc = tl_launch_append(ap, 1, st);
-            if (rc) return rc;
+            /* the prefill launch writes the rows itself (its stores address
+             * the whole layer through one 2 GB buffer resource) */
+            fused = !tl_tune(TL_TUNE_PREFILL_SEPARATE_APPEND) &&
+                    (u64)L->n_kv_head * L->cap * L->head_dim * 2 < 0x7ffffff0ull;
+            if (!fused) {
+                ap.rope = rope;
+                rc = tl_launch_append(ap, 1, st);
+                if (rc) return rc;
+            }
         }
-        return tl_launch_prefill(lv, a, rope, st);
+        return tl_launch_prefill(lv, a, rope, st, fused);
     }
     DecParams p;
     memset(&p, 0, sizeof(p));

@@ -59,7 +59,8 @@ static u32 qblocks(u32 D, u32 G) {
 }
 
 int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &rope,
-                      hipStream_t st) {
+                      hipStream_t st, bool append) {
+    if (append && L.q8) return tl_fail(TL_EINVAL, "prefill: no fused append into a Q8_0 cache");
     const u32 D = L.head_dim, G = a->n_head / L.n_kv_head;
     if (L.q8 && (!L.ks || !L.vs)) return tl_fail(TL_EINVAL, "prefill: a Q8_0 cache needs scales");
     PrefParams p;
@@ -105,13 +106,28 @@ int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &
         if (ns < 1) ns = 1;
     }
     p.n_split = ns;
-    if (ns > 1) {
+    const size_t units = (size_t)L.n_kv_head * ((a->n + TL_PF_ROWS - 1) / TL_PF_ROWS);
+    if (ns > 1 || append) {
         TlWorkspace *w;
-        size_t parts = (size_t)a->n * a->n_head * ns;
-        int rc = tl_workspace_get(st, parts * D, parts, 0, &w);
+        size_t parts = ns > 1 ? (size_t)a->n * a->n_head * ns : 0;
+        /* fused append: launch counter and unit flags past the decode
+         * merge's counters */
+        int rc = tl_workspace_get(st, parts * D, parts,
+                                  append ? TL_MERGE_CNT_WORDS + TL_PF_CTR_WORDS + units : 0, &w);
         if (rc) return rc;
-        p.ws_acc = w->acc;
-        p.ws_ml = (float2 *)w->ml;
+        if (ns > 1) {
+            p.ws_acc = w->acc;
+            p.ws_ml = (float2 *)w->ml;
+        }
+        if (append) {
+            p.kin = a->k;
+            p.vin = a->v;
+            p.kv_stride = a->kv_stride;
+            p.ctr = w->cnt + TL_MERGE_CNT_WORDS;
+            p.flags = p.ctr + TL_PF_CTR_WORDS;
+            const u32 polls = tl_tune(TL_TUNE_PREFILL_APPEND_POLLS);
+            p.polls = polls ? polls - 1 : 4096;
+        }
     }
     const u32 blocks = base * ns;
     const bool rope_on = rope.rdim != 0;

@@ -74,6 +74,52 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     const int h = lane >> 5;             /* half-wave */
     const int lr = lane & 31;
 
+    /* ---- fused append ----
+     * The batch rows go into the cache at the launch's start, before any
+     * workgroup reads the cache: workgroup b writes units b, b + grid, ...
+     * (a unit = TL_PF_ROWS rows of one kv-head, the same conversion and
+     * rotation as kv_append_kernel), waits for its stores, and sets the
+     * units' flags to this launch's epoch (below: await_batch).  Stores and
+     * flags cross XCDs with the device-coherent policy. */
+    const bool fa = !Q8 && p.kin != nullptr;
+    const u32 n_units = (p.n + TL_PF_ROWS - 1) / TL_PF_ROWS;
+    u32 epoch = 0;
+    __shared__ u32 s_direct;
+    /* unit (kvh_u, rows r0..r0+TL_PF_ROWS) of the batch into the cache */
+    auto write_unit = [&](u32 kvh_u, u32 r0) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rkw = buf_rsrc(p.k), rvw = buf_rsrc(p.v);
+        constexpr int IPU = TL_PF_ROWS * CPR;             /* 16-byte items per unit */
+        for (int i = tid; i < IPU; i += T) {
+            const u32 row = r0 + (u32)(i / CPR), c = (u32)(i % CPR);
+            if (row >= p.n) continue;
+            const u32 key = p.pos + row;
+            const u32 ph = p.ring ? key % p.ring : (p.slots ? p.slots[key] : key);
+            if (ph >= p.cap) continue;
+            const float *kr = p.kin + (u64)row * p.kv_stride + (u64)kvh_u * D;
+            const float *vr = p.vin + (u64)row * p.kv_stride + (u64)kvh_u * D;
+            const uint4 kk = ROPE ? cvt8_rope(kr, c * 8, key, p.rope.rdim, p.rope.theta,
+                                              p.rope.neox)
+                                  : cvt8_f16(kr + c * 8);
+            const uint4 vv = cvt8_f16(vr + c * 8);
+            const u32 off = (u32)((((u64)kvh_u * p.cap + ph) * D + c * 8) * 2);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4v_t{kk.x, kk.y, kk.z, kk.w}, rkw, off, 0,
+                                                   TL_SC1);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4v_t{vv.x, vv.y, vv.z, vv.w}, rvw, off, 0,
+                                                   TL_SC1);
+        }
+    };
+    if (fa) {
+        epoch = __builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(p.ctr), 0u, 0, TL_SC1) + 1u;
+        for (u32 u = blockIdx.x; u < p.n_kv * n_units; u += gridDim.x)
+            write_unit(u / n_units, (u % n_units) * TL_PF_ROWS);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (tid == 0) s_direct = 0u;
+        __syncthreads();
+        for (u32 u = blockIdx.x + (u32)tid * gridDim.x; u < p.n_kv * n_units;
+             u += (u32)T * gridDim.x)
+            __hip_atomic_store(&p.flags[u], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     /* block -> (K/V range x = kvh * n_split + split, query block); blocks that
      * read the same K/V range sit on the same XCD (block b runs on XCD b % 8) */
     const u32 nx = p.n_kv * p.n_split;
@@ -181,6 +227,32 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
             rows_next[j] = __builtin_amdgcn_raw_buffer_load_b32(rslots, key * 4u, 0, 0);
         }
     };
+    /* fused append: a workgroup whose keys reach the batch rows waits
+     * (bounded) for the flags of every unit of its kv-head up to its last
+     * key; units whose flag does not come (a writer not resident) it writes
+     * itself (the same bytes).  Its tile loads stay plain: no CU or L2 of
+     * this launch has read a batch row's cache lines before its flag (a row
+     * is whole 128-byte lines, its slot holds no older position read here,
+     * and the launch starts with the caches invalidated), and the writers'
+     * stores were written through before their flags were set. */
+    auto await_batch = [&]() __attribute__((always_inline)) {
+        const u32 need = (wg_last - p.pos + TL_PF_ROWS - 1) / TL_PF_ROWS;
+        if ((u32)tid < need) {
+            const u32 *fl = p.flags + kvh * n_units + (u32)tid;
+            bool ok = false;
+            for (u32 it = 0; it < p.polls && !ok; it++) {
+                if (it) __builtin_amdgcn_s_sleep(4);
+                ok = __hip_atomic_load(fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+            }
+            if (!ok) s_direct = 1u;
+        }
+        __syncthreads();
+        if (s_direct) {
+            for (u32 b = 0; b < need; b++) write_unit(kvh, b * TL_PF_ROWS);
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
+    };
     auto load_tile = [&](u32 tb, int s) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) {
@@ -233,6 +305,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     const int tr_row = li >> 2;                       /* + 4h (+8) + 16 kb4 */
     const int tr_col = 16 * (gi & 1) + 4 * (li & 3);  /* + 32 b */
 
+    /* the workgroup reads batch rows: all their units must be in the cache
+     * before its first load (the writers published at their start) */
+    if (fa && ke > p.pos) await_batch();
     if (ks < ke) {
         fetch_rows(ks);
         load_tile(ks, 0);
@@ -372,6 +447,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * PCfg<D, G>::W, 64 * P
     }
     lsum += __shfl_xor(lsum, 32);
 
+    /* the launch's last workgroup to finish advances the epoch: every
+     * workgroup has read it by then */
+    if (fa && tid == 0 &&
+        __hip_atomic_fetch_add(p.ctr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            gridDim.x - 1) {
+        __hip_atomic_store(p.ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(p.ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (!row_ok) return;
     /* o[b][r] = O^T[d = 32b + 8(r/4) + 4h + r%4][row lr] */
     if (p.n_split == 1) {
