@@ -230,6 +230,24 @@ def test_attn_full_size_vs_oracle(T, case):
     assert np.abs(out - o32).max() < TOL
 
 
+@pytest.mark.parametrize("tile", ["vector", "matrix"])
+@pytest.mark.parametrize("case", ATTN_CASES + [c[:5] + (1,) + c[5:] for c in FULL_SIZE_CASES])
+def test_decode_tile_paths_vs_oracle(T, case, tile):
+    """Both decode tile computations (v_dot2 on the vector ALUs, v_mfma
+    16x16 on the matrix cores), forced whatever the automatic choice for the
+    shape, within tolerance of the oracle and of each other."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n, window, perm = case[:8]
+    ring = case[8] if len(case) > 8 else 0
+    rng = np.random.default_rng(pos + 17 * n)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    with tlkv.tuning(tlkv.TUNE_DECODE_MFMA, 1 if tile == "vector" else 2):
+        out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                        seed=pos + n, ring=ring)
+    assert np.abs(out - o16).max() < TOL
+    assert np.abs(out - o32).max() < TOL
+
+
 def test_attn_noncontiguous_equals_contiguous(T):
     """Spec'd parity test of the reference design (slot table [7,3,9,12] vs
     [0,1,2,3]): identical outputs."""

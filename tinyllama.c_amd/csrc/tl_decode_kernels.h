@@ -387,6 +387,113 @@ TL_DEV void ring_tile_q8(const uint4 *tk, const uint4 *tv, const u16 *sk, const 
     }
 }
 
+/* ---- matrix-core tile (MF instances) ----
+ * The same staged tile (row t, chunk c at LDS unit t*CPR + (c ^ (t & 1)))
+ * computed on v_mfma 16x16 tiles with the G heads of the group as the
+ * columns (16 - G columns carry q = 0 and are never written out):
+ *   S^T[key][head] = K . Q^T   v_mfma_f32_16x16x32_f16 per 16-key block and
+ *                              32 dims: A = 8 dims of key row (lane & 15)
+ *                              (chunk 4j + lane/16), B = the same dims of q
+ *                              (registers);
+ *   O^T[dim][head] += V^T . P^T  v_mfma_f32_16x16x16f16 per 16-key block and
+ *                              16 dims: A = V^T read with ds_read_b64_tr_b16,
+ *                              B = the block's probabilities exactly as the
+ *                              S accumulator leaves them (lane holds keys
+ *                              4*(lane/16) + i of head lane & 15).
+ * A lane owns one head column: its running max m (common to the column's
+ * four lanes), its share l of the column's sum and D/4 output dims, so the
+ * rescale and the final combine need no cross-lane moves besides the
+ * column max of each tile (two shuffles).  Tiles of 8 keys (head_dim 256)
+ * fill the block's other 8 rows with copies whose scores are masked. */
+typedef _Float16 dh8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 dh4_t __attribute__((ext_vector_type(4)));
+typedef float df4_t __attribute__((ext_vector_type(4)));
+typedef short ds4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) ds4_t lds_ds4_t;
+
+TL_DEV dh8_t u4_as_h8(uint4 v) {
+    const u32x4_t t = {v.x, v.y, v.z, v.w};
+    return __builtin_bit_cast(dh8_t, t);
+}
+
+/* within each 16-lane group, lane i receives element (i & 3) of the 4-half
+ * vector addressed by lane 4e + (i >> 2), e = 0..3 (a 4x16 -> 16x4
+ * transpose when lane j addresses row j >> 2, columns 4 (j & 3) ..) */
+TL_DEV dh4_t ld_tr16_h4(const _Float16 *lds_ptr) {
+    const ds4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ds4_t *)(lds_ptr));
+    return __builtin_bit_cast(dh4_t, v);
+}
+
+template <int D, int G>
+TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32], u32 tbase,
+                      u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+    using C = RCfg<D>;
+    constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32, DB = D / 16;
+    constexpr float NEG_INF = -__builtin_huge_valf();
+    const int g = lane >> 4, c = lane & 15;
+    df4_t s[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int t = (16 * b + c) % TK;
+        df4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < QS; j++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u4_as_h8(tk[t * CPR + ((4 * j + g) ^ (t & 1))]),
+                                                         qb[j], acc, 0, 0, 0);
+        s[b] = acc;
+    }
+    /* keys past the chunk (wave-uniform: only a chunk's last tile) and the
+     * copied rows of 8-key tiles */
+    if (TK < 16 || tbase + (u32)TK > kend) {
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const u32 kk = (u32)(16 * b + 4 * g + i);
+                if (kk >= (u32)TK || tbase + kk >= kend) s[b][i] = NEG_INF;
+            }
+    }
+    float mx = NEG_INF;
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[b][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (__builtin_amdgcn_ballot_w64(mx > m + TL_DEC_TAU)) {
+        /* rare: move the column's reference to this tile's max */
+        const bool mv = mx > m + TL_DEC_TAU;
+        const float a = mv ? fast_exp2(m - mx) : 1.f;
+        m = mv ? mx : m;
+        l *= a;
+#pragma unroll
+        for (int db = 0; db < DB; db++) O[db] *= a;
+    }
+    const float mu = (m == NEG_INF) ? 0.f : m;
+    dh4_t pb[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p[i] = fast_exp2(s[b][i] - mu);
+            l += p[i];
+        }
+        pb[b] = dh4_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+    }
+    const _Float16 *vh = (const _Float16 *)tv;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int t = (16 * b + 4 * g + (c >> 2)) % TK;
+#pragma unroll
+        for (int db = 0; db < DB; db++) {
+            const int x = 16 * db + 4 * (c & 3);
+            const dh4_t va = ld_tr16_h4(vh + (t * CPR + ((x >> 3) ^ (t & 1))) * 8 + (x & 7));
+            O[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb[b], O[db], 0, 0, 0);
+        }
+    }
+}
+
 constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 : x >= 2 ? 2 : 1; }
 
 /* Merge of a group's n_split partials by its last workgroup, in registers:
@@ -535,8 +642,9 @@ TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq
  * from registers after the ring has drained. */
 #define TL_RING_WAVES 8
 #define TL_RING_STAGES 2
-template <int D, int G, bool ROPE, bool Q8>
+template <int D, int G, bool ROPE, bool Q8, bool MF>
 __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
+    static_assert(!(MF && Q8), "the matrix-core tile reads f16 tiles");
     using C = RCfg<D>;
     constexpr int LPK = C::LPK, CPR = C::CPR, TK = C::TK, UNITS = C::UNITS, LD = C::LD;
     /* a Q8_0 tile is half the bytes of an f16 one: twice the stages in the
@@ -826,6 +934,18 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 #pragma unroll
         for (int e = 0; e < 16; e++) acc[h][e] = 0.f;
     }
+    /* MF: q as the QK B operand (head lane & 15, chunk 4j + lane / 16; zero
+     * past the group's heads) and one head column's state per lane */
+    dh8_t qm[MF ? D / 32 : 1];
+    df4_t O1[MF ? D / 16 : 1];
+    float m1 = NEG_INF, l1 = 0.f;
+    if constexpr (MF) {
+        const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < D / 32; j++) qm[j] = c < G ? u4_as_h8(s_q[c * CPR + 4 * j + g]) : dh8_t{};
+#pragma unroll
+        for (int db = 0; db < D / 16; db++) O1[db] = df4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
     for (u32 j = 0; j < nj; j++) {
         const u32 after = nj - 1 - j;
@@ -838,6 +958,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
             ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
                                kend, lane, m, l, acc);
+        } else if constexpr (MF) {
+            mfma_tile<D, G>(st, st + UNITS, qm, kbeg + (wave + W * j) * TK, kend, lane, m1, l1, O1);
         } else {
             ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
         }
@@ -868,7 +990,10 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             tv[u] = b;
         }
         __builtin_amdgcn_wave_barrier();
-        ring_tile<D, G>(tk, tv, qr, tb, kend, lane, m, l, acc);
+        if constexpr (MF)
+            mfma_tile<D, G>(tk, tv, qm, tb, kend, lane, m1, l1, O1);
+        else
+            ring_tile<D, G>(tk, tv, qr, tb, kend, lane, m, l, acc);
         __builtin_amdgcn_wave_barrier();
     }
     if (!Q8 && writer) {
@@ -883,148 +1008,196 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         }
     }
 
-    /* ---- one state per workgroup and head ----
-     * The running max is wave-uniform, so the lanes of a wave add directly;
-     * the waves combine with weights exp2(m_w - M_h).  The lane groups of a
-     * DPP row are added in registers first; then a wave writes its state
-     * into its own ring region (no barrier: that region is no longer read):
-     * acc as float4 [head][k4][row-sum lane] (up to HB heads, 16 KB), l per
-     * remaining lane group.  After one barrier, TPC threads per output
-     * float4 each add a share of the W * GV lane groups (lanes sub +
-     * LPK*part: every 8-lane phase of a read touches distinct banks), then
-     * add across with shuffles.  More than HB heads take further rounds
-     * through the same memory. */
-    /* lane groups of one DPP row (16 lanes) are first added in registers
-     * (row rotations by 8, then 4), so only one group per row goes through
-     * LDS: PRE rotation steps, LV lanes per wave written, GV groups each */
-    constexpr int PRE = LPK == 8 ? 1 : LPK == 4 ? 2 : 0;
-    constexpr int LV = 64 >> PRE;
-    constexpr int GV = LV / LPK;                      /* lane groups per wave in LDS */
-    constexpr int NGRP = W * GV;                      /* lane groups per workgroup */
-    constexpr int WREG = RING_U;                      /* float4 per wave region */
-    constexpr int HB0 = WREG / (4 * LV);              /* heads that fit one round */
-    constexpr int HB = G < HB0 ? G : HB0;             /* heads per round */
-    constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
-    constexpr int TPC0 = NT / COLB > GV ? GV : NT / COLB;
-    constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
-    static_assert(HB * 4 * LV <= WREG, "wave state exceeds its ring region");
-    static_assert(GV % TPC == 0, "lane groups per thread");
-    if constexpr (PRE >= 1) {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            l[h] += dpp_f<DPP_ROW_ROR8>(l[h]);
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[h][e] += dpp_f<DPP_ROW_ROR8>(acc[h][e]);
-        }
-    }
-    if constexpr (PRE >= 2) {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            l[h] += dpp_f<DPP_ROW_ROR4>(l[h]);
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[h][e] += dpp_f<DPP_ROW_ROR4>(acc[h][e]);
-        }
-    }
-    /* lanes that hold their row's sums, and their place among them */
-    const bool vlane = (lane & (PRE == 2 ? 12 : PRE == 1 ? 8 : 0)) == 0;
-    const int ci = PRE == 0 ? lane : (lane % LPK) | ((lane >> 4) * LPK);
-    __shared__ float s_lg[G][NGRP];
-    __shared__ float2 s_rec[G];
-    float4 *s_w4 = (float4 *)&s_ring[0][0];
-    const int sub = lane % LPK, gv = ci / LPK;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        if (vlane) {
-            if constexpr (own_head_softmax<G, LPK>()) {
-                if (sub == h) s_lg[h][wave * GV + gv] = l[0];
-            } else {
-                if (sub == 0) s_lg[h][wave * GV + gv] = l[h];
-            }
-        }
-        if (lane == 0) s_m[wave][h] = m[h];
-    }
+    /* ---- one state per workgroup and head, then its output or partial ---- */
     const bool single = (n_split == 1);
     const bool last_merges = p.counters != nullptr;
     const u32 pb = (grow * p.n_head + kvh * G) * n_split;
-    /* reader mapping: t -> (sub, part, k4, hh) */
-    const int rsub = tid % LPK, rpart = (tid / LPK) % TPC, rest = tid / (LPK * TPC);
-    const int rk4 = rest % 4, rhh = rest / 4;
+    __shared__ float2 s_rec[G];
+    /* output float4 (head h, dims d..d+3) of the workgroup's state: the
+     * result itself (one split) or the split's partial */
+    auto emit = [&](int h, int d, float mm, float L, float4 O) __attribute__((always_inline)) {
+        const u32 hq = kvh * G + h;
+        if (single) {
+            const float inv = 1.0f / L;
+            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] =
+                make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+        } else if (last_merges) {
+            /* device-coherent stores: the merging workgroup may run
+             * on another XCD and reads them with device-coherent loads */
+            const u32 pi = (u32)h * n_split + split;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4v_t{__float_as_uint(O.x), __float_as_uint(O.y), __float_as_uint(O.z),
+                         __float_as_uint(O.w)},
+                buf_rsrc(p.ws_acc + (u64)pb * D), (pi * D + d) * 4, 0, TL_SC1);
+            if (d == 0) {
+                if (p.dist)
+                    s_rec[h] = make_float2(mm, L);   /* record written below */
+                else
+                    __builtin_amdgcn_raw_buffer_store_b64(
+                        u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
+                        buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
+            }
+        } else {
+            const u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
+            *(float4 *)&p.ws_acc[pi * D + d] = O;
+            if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
+        }
+    };
+    if constexpr (MF) {
+        /* a column's sum over its four lanes; then every wave writes its
+         * heads' (m, l) and O^T rows into its own ring region (no barrier:
+         * that region is no longer read), and after one barrier thread
+         * (h, d4) combines the waves with weights exp2(m_w - M_h) */
+        __shared__ float s_lw[MF ? G : 1][W];
+        const int c = lane & 15, g = lane >> 4;
+        l1 += __shfl_xor(l1, 16);
+        l1 += __shfl_xor(l1, 32);
+        float *so = (float *)&s_ring[wave][0];
+        static_assert(G * D * 4 <= RING_U * 16, "wave state exceeds its ring region");
+        if (c < G) {
 #pragma unroll
-    for (int h0 = 0; h0 < G; h0 += HB) {
-        if (h0) __syncthreads();                      /* previous round read */
-        float4 *mine = s_w4 + wave * WREG;
-        if (vlane)
-#pragma unroll
-            for (int hh = 0; hh < HB; hh++)
-                if (h0 + hh < G)
-#pragma unroll
-                    for (int k4 = 0; k4 < 4; k4++)
-                        mine[(hh * 4 + k4) * LV + ci] =
-                            make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
-                                        acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
+            for (int db = 0; db < D / 16; db++)
+                *(float4 *)&so[c * D + 16 * db + 4 * g] =
+                    make_float4(O1[db][0], O1[db][1], O1[db][2], O1[db][3]);
+            if (g == 0) {
+                s_m[wave][c] = m1;
+                s_lw[c][wave] = l1;
+            }
+        }
         __syncthreads();
-        const int h = h0 + rhh;
-        if (rhh < HB && h < G) {
-            const int d = rsub * 16 + rk4 * 4;
+        if (tid < G * D / 4) {
+            const int h = tid / (D / 4), d = (tid % (D / 4)) * 4;
             float mm = s_m[0][h];
 #pragma unroll
             for (int w = 1; w < W; w++) mm = fmaxf(mm, s_m[w][h]);
             const float mu = (mm == NEG_INF) ? 0.f : mm;
             float L = 0.f;
             float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 *src = s_w4 + (rhh * 4 + rk4) * LV + rsub;
 #pragma unroll
             for (int w = 0; w < W; w++) {
                 const float e = fast_exp2(s_m[w][h] - mu);
-                float lw = 0.f;
-                float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int g = 0; g < GV; g += TPC) {
-                    const float4 t = src[w * WREG + (g + rpart) * LPK];
-                    lw += s_lg[h][w * GV + g + rpart];
-                    a.x += t.x; a.y += t.y; a.z += t.z; a.w += t.w;
-                }
-                L = fmaf(e, lw, L);
-                O.x = fmaf(e, a.x, O.x);
-                O.y = fmaf(e, a.y, O.y);
-                O.z = fmaf(e, a.z, O.z);
-                O.w = fmaf(e, a.w, O.w);
+                const float4 t = *(const float4 *)((const float *)&s_ring[w][0] + h * D + d);
+                L = fmaf(e, s_lw[h][w], L);
+                O.x = fmaf(e, t.x, O.x);
+                O.y = fmaf(e, t.y, O.y);
+                O.z = fmaf(e, t.z, O.z);
+                O.w = fmaf(e, t.w, O.w);
             }
-#pragma unroll
-            for (int x = LPK; x < LPK * TPC; x *= 2) {
-                L += __shfl_xor(L, x);
-                O.x += __shfl_xor(O.x, x);
-                O.y += __shfl_xor(O.y, x);
-                O.z += __shfl_xor(O.z, x);
-                O.w += __shfl_xor(O.w, x);
+            emit(h, d, mm, L, O);
+        }
+    } else {
+        /* ---- one state per workgroup and head ----
+         * The running max is wave-uniform, so the lanes of a wave add directly;
+         * the waves combine with weights exp2(m_w - M_h).  The lane groups of a
+         * DPP row are added in registers first; then a wave writes its state
+         * into its own ring region (no barrier: that region is no longer read):
+         * acc as float4 [head][k4][row-sum lane] (up to HB heads, 16 KB), l per
+         * remaining lane group.  After one barrier, TPC threads per output
+         * float4 each add a share of the W * GV lane groups (lanes sub +
+         * LPK*part: every 8-lane phase of a read touches distinct banks), then
+         * add across with shuffles.  More than HB heads take further rounds
+         * through the same memory. */
+        /* lane groups of one DPP row (16 lanes) are first added in registers
+         * (row rotations by 8, then 4), so only one group per row goes through
+         * LDS: PRE rotation steps, LV lanes per wave written, GV groups each */
+        constexpr int PRE = LPK == 8 ? 1 : LPK == 4 ? 2 : 0;
+        constexpr int LV = 64 >> PRE;
+        constexpr int GV = LV / LPK;                      /* lane groups per wave in LDS */
+        constexpr int NGRP = W * GV;                      /* lane groups per workgroup */
+        constexpr int WREG = RING_U;                      /* float4 per wave region */
+        constexpr int HB0 = WREG / (4 * LV);              /* heads that fit one round */
+        constexpr int HB = G < HB0 ? G : HB0;             /* heads per round */
+        constexpr int COLB = HB * D / 4;                  /* float4 columns per round */
+        constexpr int TPC0 = NT / COLB > GV ? GV : NT / COLB;
+        constexpr int TPC = pow2_floor(TPC0 < 1 ? 1 : TPC0);   /* threads per column */
+        static_assert(HB * 4 * LV <= WREG, "wave state exceeds its ring region");
+        static_assert(GV % TPC == 0, "lane groups per thread");
+        if constexpr (PRE >= 1) {
+    #pragma unroll
+            for (int h = 0; h < G; h++) {
+                l[h] += dpp_f<DPP_ROW_ROR8>(l[h]);
+    #pragma unroll
+                for (int e = 0; e < 16; e++) acc[h][e] += dpp_f<DPP_ROW_ROR8>(acc[h][e]);
             }
-            if (rpart == 0) {
-                const u32 hq = kvh * G + h;
-                if (single) {
-                    const float inv = 1.0f / L;
-                    *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] =
-                        make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
-                } else if (last_merges) {
-                    /* device-coherent stores: the merging workgroup may run
-                     * on another XCD and reads them with device-coherent loads */
-                    const u32 pi = (u32)h * n_split + split;
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        u32x4v_t{__float_as_uint(O.x), __float_as_uint(O.y), __float_as_uint(O.z),
-                                 __float_as_uint(O.w)},
-                        buf_rsrc(p.ws_acc + (u64)pb * D), (pi * D + d) * 4, 0, TL_SC1);
-                    if (d == 0) {
-                        if (p.dist)
-                            s_rec[h] = make_float2(mm, L);   /* record written below */
-                        else
-                            __builtin_amdgcn_raw_buffer_store_b64(
-                                u32x2v_t{__float_as_uint(mm), __float_as_uint(L)},
-                                buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
-                    }
+        }
+        if constexpr (PRE >= 2) {
+    #pragma unroll
+            for (int h = 0; h < G; h++) {
+                l[h] += dpp_f<DPP_ROW_ROR4>(l[h]);
+    #pragma unroll
+                for (int e = 0; e < 16; e++) acc[h][e] += dpp_f<DPP_ROW_ROR4>(acc[h][e]);
+            }
+        }
+        /* lanes that hold their row's sums, and their place among them */
+        const bool vlane = (lane & (PRE == 2 ? 12 : PRE == 1 ? 8 : 0)) == 0;
+        const int ci = PRE == 0 ? lane : (lane % LPK) | ((lane >> 4) * LPK);
+        __shared__ float s_lg[G][NGRP];
+        float4 *s_w4 = (float4 *)&s_ring[0][0];
+        const int sub = lane % LPK, gv = ci / LPK;
+    #pragma unroll
+        for (int h = 0; h < G; h++) {
+            if (vlane) {
+                if constexpr (own_head_softmax<G, LPK>()) {
+                    if (sub == h) s_lg[h][wave * GV + gv] = l[0];
                 } else {
-                    const u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
-                    *(float4 *)&p.ws_acc[pi * D + d] = O;
-                    if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
+                    if (sub == 0) s_lg[h][wave * GV + gv] = l[h];
                 }
+            }
+            if (lane == 0) s_m[wave][h] = m[h];
+        }
+        /* reader mapping: t -> (sub, part, k4, hh) */
+        const int rsub = tid % LPK, rpart = (tid / LPK) % TPC, rest = tid / (LPK * TPC);
+        const int rk4 = rest % 4, rhh = rest / 4;
+    #pragma unroll
+        for (int h0 = 0; h0 < G; h0 += HB) {
+            if (h0) __syncthreads();                      /* previous round read */
+            float4 *mine = s_w4 + wave * WREG;
+            if (vlane)
+    #pragma unroll
+                for (int hh = 0; hh < HB; hh++)
+                    if (h0 + hh < G)
+    #pragma unroll
+                        for (int k4 = 0; k4 < 4; k4++)
+                            mine[(hh * 4 + k4) * LV + ci] =
+                                make_float4(acc[h0 + hh][4 * k4], acc[h0 + hh][4 * k4 + 1],
+                                            acc[h0 + hh][4 * k4 + 2], acc[h0 + hh][4 * k4 + 3]);
+            __syncthreads();
+            const int h = h0 + rhh;
+            if (rhh < HB && h < G) {
+                const int d = rsub * 16 + rk4 * 4;
+                float mm = s_m[0][h];
+    #pragma unroll
+                for (int w = 1; w < W; w++) mm = fmaxf(mm, s_m[w][h]);
+                const float mu = (mm == NEG_INF) ? 0.f : mm;
+                float L = 0.f;
+                float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 *src = s_w4 + (rhh * 4 + rk4) * LV + rsub;
+    #pragma unroll
+                for (int w = 0; w < W; w++) {
+                    const float e = fast_exp2(s_m[w][h] - mu);
+                    float lw = 0.f;
+                    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    #pragma unroll
+                    for (int g = 0; g < GV; g += TPC) {
+                        const float4 t = src[w * WREG + (g + rpart) * LPK];
+                        lw += s_lg[h][w * GV + g + rpart];
+                        a.x += t.x; a.y += t.y; a.z += t.z; a.w += t.w;
+                    }
+                    L = fmaf(e, lw, L);
+                    O.x = fmaf(e, a.x, O.x);
+                    O.y = fmaf(e, a.y, O.y);
+                    O.z = fmaf(e, a.z, O.z);
+                    O.w = fmaf(e, a.w, O.w);
+                }
+    #pragma unroll
+                for (int x = LPK; x < LPK * TPC; x *= 2) {
+                    L += __shfl_xor(L, x);
+                    O.x += __shfl_xor(O.x, x);
+                    O.y += __shfl_xor(O.y, x);
+                    O.z += __shfl_xor(O.z, x);
+                    O.w += __shfl_xor(O.w, x);
+                }
+                if (rpart == 0) emit(h, d, mm, L, O);
             }
         }
     }

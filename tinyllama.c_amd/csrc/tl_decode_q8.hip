@@ -11,8 +11,8 @@ static DecKernel pick_q8(int G, bool rope) {
     switch (G) {
 #define TL_CASE(g)                                                                               \
     case g:                                                                                      \
-        if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true, true>, 4096, NT};    \
-        return {(const void *)attn_decode_ring_kernel<D, g, false, true>, 4096, NT};
+        if (rope) return {(const void *)attn_decode_ring_kernel<D, g, true, true, false>, 4096, NT};    \
+        return {(const void *)attn_decode_ring_kernel<D, g, false, true, false>, 4096, NT};
         TL_CASE(1) TL_CASE(2) TL_CASE(3) TL_CASE(4)
         TL_CASE(5) TL_CASE(6) TL_CASE(7) TL_CASE(8)
 #undef TL_CASE
