@@ -638,8 +638,9 @@ TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq
  * the stream loop); the groups and waves merge once at the end.  Split
  * decomposition, XCD-aware block order, GQA sharing, the fused append and
  * the split merge are described at the top of this file.  Tiles that hold rows
- * appended by this launch (the last tiles of the last split) are filled
- * from registers after the ring has drained. */
+ * appended by this launch (the last tiles of the last split) stream through
+ * the ring like the others; their new rows are then overwritten in LDS with
+ * the rows staged from the f32 input. */
 #define TL_RING_WAVES 8
 #define TL_RING_STAGES 2
 template <int D, int G, bool ROPE, bool Q8, bool MF>
@@ -861,13 +862,14 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const u16 *VS = Q8 ? sq.vs + (u64)kvh * sq.cap * (D / 32) : nullptr;
     const u32 scl_lds = (u32)(uintptr_t)&s_scl[Q8 ? wave : 0][0];
 
-    /* tiles of the chunk: the first n_dma (entirely cache rows written
-     * before this launch) stream through the ring; the rest hold new rows */
+    /* tiles of the chunk, all streamed through the ring; rows appended by
+     * this launch (key >= pos) are read from memory too (stale or new: the
+     * writer may be storing them now) and replaced in LDS by the staged new
+     * rows before the tile is used */
     const u32 ntile = (kend > kbeg) ? (kend - kbeg + TK - 1) / TK : 0;
-    u32 n_dma = ntile;
-    if (fused && kend > sq.pos) n_dma = sq.pos > kbeg ? (sq.pos - kbeg) / TK : 0;
-    const u32 nj = n_dma > (u32)wave ? (n_dma - wave + W - 1) / W : 0;   /* this wave's ring tiles */
+    const u32 nj = ntile > (u32)wave ? (ntile - wave + W - 1) / W : 0;   /* this wave's ring tiles */
     const u32 klast = kend - 1;
+    const bool patch = fused && klast >= sq.pos;
 
     auto phys = [&](u32 key) -> u32 {
         if (sq.ring) return key % sq.ring;
@@ -954,6 +956,26 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         else
             wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
         const uint4 *st = &s_ring[wave][(j % S) * STAGE_U];
+        if constexpr (!Q8) {
+            const u32 tb = kbeg + (wave + W * j) * TK;
+            if (patch && tb + TK > sq.pos) {
+                /* unit u holds chunk (u % CPR) ^ (row & 1) of row u / CPR;
+                 * rows past the chunk hold a copy of its last row */
+                uint4 *sw = &s_ring[wave][(j % S) * STAGE_U];
+#pragma unroll
+                for (int jj = 0; jj < LD; jj++) {
+                    const int u = jj * 64 + lane;
+                    const int row = u / CPR;
+                    const u32 key = min(tb + (u32)row, klast);
+                    if (key >= sq.pos) {
+                        const int c = (u % CPR) ^ (row & 1);
+                        sw[u] = s_newk[key - sq.pos][c];
+                        sw[UNITS + u] = s_newv[key - sq.pos][c];
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
         if constexpr (Q8) {
             const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
             ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
@@ -964,37 +986,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
         }
         if (j + S < nj) issue(j + S);
-    }
-    /* tiles with new rows: cache rows and staged new rows through registers */
-    if constexpr (!Q8)
-    for (u32 t = n_dma + ((u32)wave + W - n_dma % W) % W; t < ntile; t += W) {
-        uint4 *tk = &s_ring[wave][0];
-        uint4 *tv = &s_ring[wave][UNITS];
-        const u32 tb = kbeg + t * TK;
-#pragma unroll
-        for (int jj = 0; jj < LD; jj++) {
-            const int u = jj * 64 + lane;
-            const int row = u / CPR;
-            const u32 key = min(tb + (u32)row, klast);
-            const int c = (u % CPR) ^ (row & 1);
-            uint4 a, b;
-            if (key >= sq.pos) {
-                a = s_newk[key - sq.pos][c];
-                b = s_newv[key - sq.pos][c];
-            } else {
-                const u32 ph = phys(key);
-                a = ld_stream(Kbase + (u64)ph * D + c * 8);
-                b = ld_stream(Vbase + (u64)ph * D + c * 8);
-            }
-            tk[u] = a;
-            tv[u] = b;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if constexpr (MF)
-            mfma_tile<D, G>(tk, tv, qm, tb, kend, lane, m1, l1, O1);
-        else
-            ring_tile<D, G>(tk, tv, qr, tb, kend, lane, m, l, acc);
-        __builtin_amdgcn_wave_barrier();
     }
     if (!Q8 && writer) {
         for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
