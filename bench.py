@@ -664,7 +664,7 @@ def run_q8(torch, tlkv, lib, sh, gen, c, steps):
                    "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                    "f16_equivalent_GBs": round(f16_bytes / (us * 1e-6) / 1e9, 1),
                    "steps": n_st, "keys": P + 1,
-                   "kernel": "attn_decode_ring_kernel<128,4,false,true>",
+                   "kernel": "attn_decode_ring_kernel<128,4,false,true,false>",
                    "note": "tl_attn_noappend_q8 over the contiguous Q8_0 cache; GBs counts "
                            "int8 rows + f16 scales, f16_equivalent_GBs the bytes of the same "
                            "keys in the f16 cache"},
@@ -722,7 +722,7 @@ def run_state_snapshot(torch, tlkv, lib, sh):
     return out
 
 
-DECODE_KERNEL = "attn_decode_ring_kernel<128, 4, false, false>"
+DECODE_KERNEL = "attn_decode_ring_kernel<128, 4, false, false, true>"
 
 
 def split_trace(path, warmup, steps):
@@ -1035,7 +1035,7 @@ def main():
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, read "
                                        "from profiles/attn_decode_llama3-8b-32k_hbm_traffic.md "
                                        "(not measured in this run)",
-                     "kernel": "attn_decode_ring_kernel<128,4,false,false> (one OP_ATTN launch, "
+                     "kernel": "attn_decode_ring_kernel<128,4,false,false,true> (one OP_ATTN launch, "
                                "split merge inside)"},
     }
     if not args.no_prefill_attn:

@@ -21,7 +21,10 @@
  *   scale*log2(e), rounded to f16), reduced over the key's lanes with DPP;
  *   each lane group keeps its own (l, acc) against a wave-uniform running
  *   max that moves only when a score exceeds it by 2^8; p is rounded to f16
- *   and PV runs as v_dot2 over key pairs of V.
+ *   and PV runs as v_dot2 over key pairs of V (head_dim 256, Q8_0).  Up to
+ *   head_dim 128 the tile runs on the matrix cores instead (mfma_tile:
+ *   S^T = K.Q^T and O^T += V^T.P^T as v_mfma 16x16 tiles, the GQA heads as
+ *   the columns, one head column's softmax state per lane).
  *   States merge across waves through LDS and across splits in the last
  *   workgroup of the group to finish (partials written with device-coherent
  *   stores, a per-group atomic counter that this workgroup resets), or in a
