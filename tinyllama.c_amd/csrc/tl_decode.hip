@@ -141,10 +141,14 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     const u64 n_groups = (u64)n_rows_total * p.n_kv;
     u32 n_split = (u32)((target + n_groups - 1) / n_groups);
     const u32 waves = (u32)K.threads / 64;
-    /* keys per split: one tile per wave, at most 128 (head_dim 64, P = 700:
-     * 128 keys per split 8.8 us vs 9.5 us at 256; fewer keys make the
-     * merge dearer than the shorter chunks save) */
-    const u32 min_keys = tuned(TL_TUNE_DECODE_MIN_KEYS, waves * tk < 128 ? waves * tk : 128);
+    /* fewest keys per split: a tile for every wave at head_dim 128, for half
+     * of them at 64 and 256, at most 128 keys (measured: head_dim 64, P =
+     * 700: 128 keys per split 8.8 us vs 9.5 us at 256, and fewer make the
+     * merge dearer than the shorter chunks save; head_dim 256, the 1024-key
+     * window of config 5's local layers: 32 keys 12.1 us per launch on
+     * average vs 12.55 at 64) */
+    const u32 min_tiles = head_dim == 128 ? waves : waves / 2;
+    const u32 min_keys = tuned(TL_TUNE_DECODE_MIN_KEYS, min_tiles * tk < 128 ? min_tiles * tk : 128);
     const u32 max_split = (max_vis + min_keys - 1) / min_keys;
     const u32 min_split = (max_vis + TL_DEC_MAX_CHUNK - 1) / TL_DEC_MAX_CHUNK;
     if (n_split > max_split) n_split = max_split;
