@@ -205,6 +205,23 @@ def test_attn_q8_vs_oracle(T, case):
     assert np.array_equal(gv, C.v) and np.array_equal(gvs, C.vs)
 
 
+@pytest.mark.parametrize("tile", ["vector", "matrix"])
+@pytest.mark.parametrize("case", [c for c in Q8_CASES if c[5] < 16] +
+                         [(32, 8, 128, 33800, 33791, 1, 0, False, 0)])
+def test_attn_q8_decode_tile_paths(T, case, tile):
+    """Both decode tile computations over the Q8_0 cache (v_dot2 on the vector
+    ALUs, v_mfma on the matrix cores), forced whatever the automatic choice
+    for the shape, within tolerance of the Q8_0 oracle."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n, window, perm, ring = case
+    rng = np.random.default_rng(pos + 31 * n)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    with tlkv.tuning(tlkv.TUNE_DECODE_MFMA, 1 if tile == "vector" else 2):
+        out, ref, _, _ = _run_attn_q8(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                      seed=pos + n, ring=ring)
+    assert np.abs(out - ref).max() < TOL
+
+
 @pytest.mark.parametrize("n", [1, 4, 40])
 def test_attn_noappend_q8(T, n):
     rng = np.random.default_rng(n)

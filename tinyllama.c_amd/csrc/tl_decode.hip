@@ -45,7 +45,7 @@
 
 template <int D>
 static DecKernel pick_kernel(int G, bool rope, bool q8, bool mf) {
-    if (q8) return tl_pick_decode_q8(D, G, rope);   /* tl_decode_q8.hip */
+    if (q8) return tl_pick_decode_q8(D, G, rope, mf);   /* tl_decode_q8.hip */
     constexpr int NT = 64 * TL_RING_WAVES;
     switch (G) {
 #define TL_CASE(g)                                                                            \
@@ -120,11 +120,17 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
             if (p.seq[i].kin) return tl_fail(TL_EINVAL, "decode: no fused append into a Q8_0 cache");
     }
     DecKernel K;
-    /* tiles on the matrix cores up to head_dim 128; at 256 (8-key tiles,
-     * half of each 16-key block padding) the vector tile is faster
-     * (measured: config 5, gqa 2: 13.1 vs 13.4 us per launch) */
+    /* tiles on the matrix cores where measured faster (8 kv-heads, 1K and
+     * 32K keys, gqa 1-8): the f16 cache at head_dim 64 and 128 from gqa 2
+     * (gqa 8: 16.3 vs 38.3 us at 32K keys; gqa 1 even); the Q8_0 cache at
+     * head_dim 64 from gqa 2 and at 128 from gqa 5 (gqa 8: 26.9 vs 57.9 us;
+     * its matrix tile holds near 26 us at 32K keys whatever the gqa, while
+     * the vector tile takes 20-26 us up to gqa 4).  At head_dim 256 (8-key
+     * tiles, half of each 16-key block padding) the vector tile is faster
+     * (config 5, gqa 2: 13.1 vs 13.4 us per launch). */
     const u32 tile_sel = tl_tune(TL_TUNE_DECODE_MFMA);
-    const bool mf = !q8 && (tile_sel == 2 || (tile_sel != 1 && head_dim <= 128));
+    const bool mf_auto = head_dim == 64 ? G >= 2 : head_dim == 128 ? G >= (q8 ? 5u : 2u) : false;
+    const bool mf = tile_sel == 2 || (tile_sel != 1 && mf_auto);
     switch (head_dim) {
     case 64: K = pick_kernel<64>((int)G, p.rope.rdim != 0, q8, mf); break;
     case 128: K = pick_kernel<128>((int)G, p.rope.rdim != 0, q8, mf); break;

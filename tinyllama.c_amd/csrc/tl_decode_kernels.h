@@ -424,24 +424,16 @@ TL_DEV dh4_t ld_tr16_h4(const _Float16 *lds_ptr) {
     return __builtin_bit_cast(dh4_t, v);
 }
 
+/* Mask, online softmax and PV of one tile's score blocks s (keys
+ * tbase + 16b + 4*(lane/16) + i of head lane & 15) against the f16 V tile tv
+ * (row t, chunk c at unit t*CPR + (c ^ (t & 1))). */
 template <int D, int G>
-TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32], u32 tbase,
-                      u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+TL_DEV void mf_softmax_pv(df4_t (&s)[(RCfg<D>::TK + 15) / 16], const uint4 *tv, u32 tbase,
+                          u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
     using C = RCfg<D>;
-    constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32, DB = D / 16;
+    constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, DB = D / 16;
     constexpr float NEG_INF = -__builtin_huge_valf();
     const int g = lane >> 4, c = lane & 15;
-    df4_t s[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const int t = (16 * b + c) % TK;
-        df4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < QS; j++)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u4_as_h8(tk[t * CPR + ((4 * j + g) ^ (t & 1))]),
-                                                         qb[j], acc, 0, 0, 0);
-        s[b] = acc;
-    }
     /* keys past the chunk (wave-uniform: only a chunk's last tile) and the
      * copied rows of 8-key tiles */
     if (TK < 16 || tbase + (u32)TK > kend) {
@@ -492,6 +484,85 @@ TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32
             O[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb[b], O[db], 0, 0, 0);
         }
     }
+}
+
+template <int D, int G>
+TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32], u32 tbase,
+                      u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+    using C = RCfg<D>;
+    constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32;
+    const int g = lane >> 4, c = lane & 15;
+    df4_t s[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int t = (16 * b + c) % TK;
+        df4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < QS; j++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u4_as_h8(tk[t * CPR + ((4 * j + g) ^ (t & 1))]),
+                                                         qb[j], acc, 0, 0, 0);
+        s[b] = acc;
+    }
+    mf_softmax_pv<D, G>(s, tv, tbase, kend, lane, m, l, O);
+}
+
+/* mfma_tile over a Q8_0 tile (int8 rows as loaded: row t at byte t*D; f16
+ * scales [TK][D/32] in sk / sv).  Scores: every 32-dim step of the QK MFMA
+ * is exactly one scale block, so the exact int8 values (f16) go into the
+ * MFMA and each step's result is scaled by its key's block scale in f32, as
+ * the vector tile does.  V: the wave reads its int8 K fragments and V rows
+ * into registers, then writes V dequantized to f16 (RNE(q * d), as the
+ * vector tile's PV operands) over the same stage, laid out like an f16 tile
+ * (4 KB: the int8 K and V halves together), and the PV step reads it as
+ * one.  The LDS operations of one wave run in order, so every lane's reads
+ * precede the overwrite. */
+template <int D, int G>
+TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t (&qb)[D / 32],
+                         u32 tbase, u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+    using C = RCfg<D>;
+    constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32, NSB = D / 32;
+    constexpr int VU = TK * CPR / 64;              /* 8-byte V units per lane */
+    const int g = lane >> 4, c = lane & 15;
+    const uint8_t *k8 = (const uint8_t *)stage, *v8 = k8 + TK * D;
+    uint2 kw[NB][QS], vw[VU];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int t = (16 * b + c) % TK;
+#pragma unroll
+        for (int j = 0; j < QS; j++) kw[b][j] = *(const uint2 *)(k8 + t * D + 8 * (4 * j + g));
+    }
+#pragma unroll
+    for (int k = 0; k < VU; k++) {
+        const int u = lane + 64 * k;
+        vw[k] = *(const uint2 *)(v8 + (u / CPR) * D + 8 * (u % CPR));
+    }
+    df4_t s[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        s[b] = df4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < QS; j++) {
+            tl_half2 h0, h1, h2, h3;
+            i8x4_to_f16(kw[b][j].x, h0, h1);
+            i8x4_to_f16(kw[b][j].y, h2, h3);
+            const u32x4_t kx = {__builtin_bit_cast(u32, h0), __builtin_bit_cast(u32, h1),
+                                __builtin_bit_cast(u32, h2), __builtin_bit_cast(u32, h3)};
+            const df4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(dh8_t, kx), qb[j], df4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tr = (16 * b + 4 * g + i) % TK;
+                s[b][i] = fmaf(acc[i], (float)__builtin_bit_cast(_Float16, sk[tr * NSB + j]), s[b][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < VU; k++) {
+        const int u = lane + 64 * k, t = u / CPR, cc = u % CPR;
+        stage[t * CPR + (cc ^ (t & 1))] = q8_dequant8(vw[k], (u32)sv[t * NSB + cc / 4]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    mf_softmax_pv<D, G>(s, stage, tbase, kend, lane, m, l, O);
 }
 
 constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 : x >= 2 ? 2 : 1; }
@@ -645,7 +716,6 @@ TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq
 #define TL_RING_STAGES 2
 template <int D, int G, bool ROPE, bool Q8, bool MF>
 __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
-    static_assert(!(MF && Q8), "the matrix-core tile reads f16 tiles");
     using C = RCfg<D>;
     constexpr int LPK = C::LPK, CPR = C::CPR, TK = C::TK, UNITS = C::UNITS, LD = C::LD;
     /* a Q8_0 tile is half the bytes of an f16 one: twice the stages in the
@@ -978,8 +1048,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         }
         if constexpr (Q8) {
             const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
-            ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
-                               kend, lane, m, l, acc);
+            if constexpr (MF)
+                mfma_tile_q8<D, G>(&s_ring[wave][(j % S) * STAGE_U], ss, ss + 64, qm,
+                                   kbeg + (wave + W * j) * TK, kend, lane, m1, l1, O1);
+            else
+                ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
+                                   kend, lane, m, l, acc);
         } else if constexpr (MF) {
             mfma_tile<D, G>(st, st + UNITS, qm, kbeg + (wave + W * j) * TK, kend, lane, m1, l1, O1);
         } else {
@@ -1319,5 +1393,5 @@ struct DecKernel {
 };
 
 /* the Q8_0 instances (tl_decode_q8.hip) */
-DecKernel tl_pick_decode_q8(int D, int G, bool rope);
+DecKernel tl_pick_decode_q8(int D, int G, bool rope, bool mf);
 
