@@ -524,7 +524,10 @@ TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t
     constexpr int VU = TK * CPR / 64;              /* 8-byte V units per lane */
     const int g = lane >> 4, c = lane & 15;
     const uint8_t *k8 = (const uint8_t *)stage, *v8 = k8 + TK * D;
+    /* every LDS read of the tile first (values, then the scales the lane
+     * needs), so the wave waits once */
     uint2 kw[NB][QS], vw[VU];
+    u16 ksc[NB][4][QS], vsc[VU];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         const int t = (16 * b + c) % TK;
@@ -536,10 +539,27 @@ TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t
         const int u = lane + 64 * k;
         vw[k] = *(const uint2 *)(v8 + (u / CPR) * D + 8 * (u % CPR));
     }
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u16 *row = sk + ((16 * b + 4 * g + i) % TK) * NSB;   /* NSB scales, 4-byte aligned */
+#pragma unroll
+            for (int j = 0; j < QS; j += 2) {
+                const u32 w = *(const u32 *)(row + j);
+                ksc[b][i][j] = (u16)(w & 0xffffu);
+                ksc[b][i][j + 1] = (u16)(w >> 16);
+            }
+        }
+#pragma unroll
+    for (int k = 0; k < VU; k++) {
+        const int u = lane + 64 * k;
+        vsc[k] = sv[(u / CPR) * NSB + (u % CPR) / 4];
+    }
     df4_t s[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        s[b] = df4_t{0.f, 0.f, 0.f, 0.f};
+        df4_t acc[QS];
 #pragma unroll
         for (int j = 0; j < QS; j++) {
             tl_half2 h0, h1, h2, h3;
@@ -547,19 +567,20 @@ TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t
             i8x4_to_f16(kw[b][j].y, h2, h3);
             const u32x4_t kx = {__builtin_bit_cast(u32, h0), __builtin_bit_cast(u32, h1),
                                 __builtin_bit_cast(u32, h2), __builtin_bit_cast(u32, h3)};
-            const df4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(dh8_t, kx), qb[j], df4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int tr = (16 * b + 4 * g + i) % TK;
-                s[b][i] = fmaf(acc[i], (float)__builtin_bit_cast(_Float16, sk[tr * NSB + j]), s[b][i]);
-            }
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dh8_t, kx), qb[j],
+                                                            df4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         }
+        s[b] = df4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < QS; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                s[b][i] = fmaf(acc[j][i], (float)__builtin_bit_cast(_Float16, ksc[b][i][j]), s[b][i]);
     }
 #pragma unroll
     for (int k = 0; k < VU; k++) {
         const int u = lane + 64 * k, t = u / CPR, cc = u % CPR;
-        stage[t * CPR + (cc ^ (t & 1))] = q8_dequant8(vw[k], (u32)sv[t * NSB + cc / 4]);
+        stage[t * CPR + (cc ^ (t & 1))] = q8_dequant8(vw[k], (u32)vsc[k]);
     }
     __builtin_amdgcn_wave_barrier();
     mf_softmax_pv<D, G>(s, stage, tbase, kend, lane, m, l, O);
