@@ -1135,6 +1135,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
          * that region is no longer read), and after one barrier thread
          * (h, d4) combines the waves with weights exp2(m_w - M_h) */
         __shared__ float s_lw[MF ? G : 1][W];
+        static_assert(G <= 16 && G * D / 4 <= NT, "one head column per lane, one output float4 per thread");
         const int c = lane & 15, g = lane >> 4;
         l1 += __shfl_xor(l1, 16);
         l1 += __shfl_xor(l1, 32);
