@@ -248,6 +248,41 @@ def test_decode_tile_paths_vs_oracle(T, case, tile):
     assert np.abs(out - o32).max() < TOL
 
 
+def _random_decode_cases(count=24, seed=2024):
+    """Seeded decode shapes over the kernel's whole parameter range: head_dim
+    64/128/256, gqa 1-8, 1-8 kv-heads, 1-15 batch rows, full / windowed /
+    ring layers, identity or permuted slot tables."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        hd = int(rng.choice([64, 128, 256]))
+        n_kv = int(rng.choice([1, 2, 4, 8]))
+        g = int(rng.integers(1, 9))
+        n = int(rng.choice([1, 1, 1, 2, 7, 15]))
+        pos = int(rng.integers(0, 3000))
+        window = int(rng.choice([0, 0, 64, 700]))
+        ring = window + n - 1 + int(rng.integers(0, 16)) if window and rng.random() < 0.5 else 0
+        cap = ring if ring else pos + n + int(rng.integers(0, 64))
+        perm = bool(rng.random() < 0.5) and not ring
+        cases.append((g * n_kv, n_kv, hd, cap, pos, n, window, perm, ring))
+    return cases
+
+
+@pytest.mark.parametrize("tile", ["vector", "matrix"])
+@pytest.mark.parametrize("case", _random_decode_cases())
+def test_decode_random_shapes_both_tiles(T, case, tile):
+    """Both decode tile paths against the oracle over seeded random shapes."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n, window, perm, ring = case
+    rng = np.random.default_rng(cap + 7 * pos)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    with tlkv.tuning(tlkv.TUNE_DECODE_MFMA, 1 if tile == "vector" else 2):
+        out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                        seed=pos + n, ring=ring)
+    assert np.abs(out - o16).max() < TOL, case
+    assert np.abs(out - o32).max() < TOL, case
+
+
 def test_attn_noncontiguous_equals_contiguous(T):
     """Spec'd parity test of the reference design (slot table [7,3,9,12] vs
     [0,1,2,3]): identical outputs."""
