@@ -808,141 +808,6 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             slot_v[j] = i < kend ? sq.slots[i] : 0u;
         }
     }
-    /* q of the GQA group (RoPE'd at pos + r when ROPE), scaled to log2 units,
-     * f16; the launch's new K/V rows (K RoPE'd at pos + row), f16 */
-    const float sc = p.scale_log2;
-    if constexpr (ROPE) {
-        /* pairs (ia, ib) of q and of the new K rows, rotated by position,
-         * and the new V rows: every thread requests its (few) items first,
-         * then rotates, converts and stores them */
-        constexpr int QI = (G * (D / 2) + NT - 1) / NT;                /* q pairs */
-        constexpr int KI = (TL_DEC_MAX_NEW * (D / 2) + NT - 1) / NT;   /* K pairs */
-        constexpr int VI = (TL_DEC_MAX_NEW * (D / 8) + NT - 1) / NT;   /* V 8-element units */
-        const u32 pairs = p.rope.rdim >> 1;
-        const u32 nkp = need_new ? p.rows_per_seq * (D / 2) : 0u;
-        const u32 nvu = need_new ? p.rows_per_seq * VPR : 0u;
-        /* element indices of pair i: rotated pairs per the RoPE variant,
-         * the rest (i >= pairs) stay adjacent */
-        auto pair_of = [&](u32 i, u32 &ia, u32 &ib) {
-            const bool rot = i < pairs;
-            ia = (rot && p.rope.neox) ? i : 2 * i;
-            ib = (rot && p.rope.neox) ? i + pairs : 2 * i + 1;
-        };
-        float qx[QI], qy[QI], kx[KI], ky[KI];
-        float4 va[VI], vc[VI];
-#pragma unroll
-        for (int j = 0; j < QI; j++) {
-            const u32 t = tid + j * NT;
-            qx[j] = qy[j] = 0.f;
-            if (t < (u32)G * (D / 2)) {
-                u32 ia, ib;
-                pair_of(t % (D / 2), ia, ib);
-                const float *row = qb + (t / (D / 2)) * D;
-                qx[j] = row[ia];
-                qy[j] = row[ib];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < KI; j++) {
-            const u32 t = tid + j * NT;
-            kx[j] = ky[j] = 0.f;
-            if (t < nkp) {
-                u32 ia, ib;
-                pair_of(t % (D / 2), ia, ib);
-                const float *src = sq.kin + (u64)(t / (D / 2)) * sq.kv_stride + (u64)kvh * D;
-                kx[j] = src[ia];
-                ky[j] = src[ib];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < VI; j++) {
-            const u32 i = tid + j * NT;
-            va[j] = vc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (i < nvu) {
-                const float *src = sq.vin + (u64)(i / VPR) * sq.kv_stride + (u64)kvh * D + (i % VPR) * 8;
-                va[j] = *(const float4 *)src;
-                vc[j] = *(const float4 *)(src + 4);
-            }
-        }
-        u16 *q16 = (u16 *)s_q;
-#pragma unroll
-        for (int j = 0; j < QI; j++) {
-            const u32 t = tid + j * NT;
-            if (t < (u32)G * (D / 2)) {
-                const u32 h = t / (D / 2), i = t % (D / 2);
-                u32 ia, ib;
-                pair_of(i, ia, ib);
-                float x = qx[j], y = qy[j];
-                if (i < pairs) {
-                    float c, sn;
-                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
-                    rope_rot(qx[j], qy[j], c, sn, x, y);
-                }
-                const u32 pk = pack_f16x2_fast(x * sc, y * sc);
-                q16[h * D + ia] = (u16)(pk & 0xffffu);
-                q16[h * D + ib] = (u16)(pk >> 16);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < KI; j++) {
-            const u32 t = tid + j * NT;
-            if (t < nkp) {
-                const u32 row = t / (D / 2), i = t % (D / 2);
-                u32 ia, ib;
-                pair_of(i, ia, ib);
-                float x = kx[j], y = ky[j];
-                if (i < pairs) {
-                    float c, sn;
-                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + row, c, sn);
-                    rope_rot(kx[j], ky[j], c, sn, x, y);
-                }
-                u16 *k16 = (u16 *)s_newk[row];
-                k16[ia] = (u16)f32_to_f16_bits(x);
-                k16[ib] = (u16)f32_to_f16_bits(y);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < VI; j++) {
-            const u32 i = tid + j * NT;
-            if (i < nvu) s_newv[i / VPR][i % VPR] = cvt8_f16_regs(va[j], vc[j]);
-        }
-    } else {
-        /* one q item and at most one new-row item per thread (G * D / 8 and
-         * TL_DEC_MAX_NEW * D / 8 are at most NT): all loads first */
-        static_assert(G * D / 8 <= NT && TL_DEC_MAX_NEW * (D / 8) <= NT, "one item per thread");
-        float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qc = qa;
-        float4 ka = qa, kc = qa, va = qa, vc = qa;
-        const bool has_q = tid < G * D / 8;
-        const bool has_new = need_new && (u32)tid < p.rows_per_seq * VPR;
-        const u32 nrow = (u32)tid / VPR, nc8 = (u32)tid % VPR;
-        if (has_q) {
-            qa = *(const float4 *)(qb + tid * 8);
-            qc = *(const float4 *)(qb + tid * 8 + 4);
-        }
-        if (has_new) {
-            const u64 src = (u64)nrow * sq.kv_stride + (u64)kvh * D + nc8 * 8;
-            ka = *(const float4 *)(sq.kin + src);
-            kc = *(const float4 *)(sq.kin + src + 4);
-            va = *(const float4 *)(sq.vin + src);
-            vc = *(const float4 *)(sq.vin + src + 4);
-        }
-        if (has_q)
-            s_q[tid] = make_uint4(pack_f16x2_fast(qa.x * sc, qa.y * sc), pack_f16x2_fast(qa.z * sc, qa.w * sc),
-                                  pack_f16x2_fast(qc.x * sc, qc.y * sc), pack_f16x2_fast(qc.z * sc, qc.w * sc));
-        if (has_new) {
-            s_newk[nrow][nc8] = cvt8_f16_regs(ka, kc);
-            s_newv[nrow][nc8] = cvt8_f16_regs(va, vc);
-        }
-    }
-    if (staged) {
-#pragma unroll
-        for (int j = 0; j < SPT; j++) {
-            const u32 i = tid + j * NT;
-            if (kbeg + i < kend) s_slot[i] = slot_v[j] < sq.cap ? slot_v[j] : 0u;
-        }
-    }
-    __syncthreads();
-
     const u16 *Kbase = sq.k + (u64)kvh * sq.cap * D;
     const u16 *Vbase = sq.v + (u64)kvh * sq.cap * D;
     const u32 ring_lds = (u32)(uintptr_t)&s_ring[wave][0];
@@ -1006,7 +871,161 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     };
 
     const u32 npre = nj < (u32)S ? nj : (u32)S;
-    for (u32 j = 0; j < npre; j++) issue(j);
+    /* the chunk's slots to LDS (one barrier), then the first tiles' loads */
+    auto stage_and_issue = [&]() __attribute__((always_inline)) {
+        if (staged) {
+#pragma unroll
+            for (int j = 0; j < SPT; j++) {
+                const u32 i = tid + j * NT;
+                if (kbeg + i < kend) s_slot[i] = slot_v[j] < sq.cap ? slot_v[j] : 0u;
+            }
+        }
+        __syncthreads();
+        for (u32 j = 0; j < npre; j++) issue(j);
+    };
+    /* q of the GQA group (RoPE'd at pos + r when ROPE), scaled to log2 units,
+     * f16; the launch's new K/V rows (K RoPE'd at pos + row), f16 */
+    const float sc = p.scale_log2;
+    if constexpr (ROPE) {
+        /* pairs (ia, ib) of q and of the new K rows, rotated by position,
+         * and the new V rows: every thread requests its (few) items first,
+         * then rotates, converts and stores them */
+        constexpr int QI = (G * (D / 2) + NT - 1) / NT;                /* q pairs */
+        constexpr int KI = (TL_DEC_MAX_NEW * (D / 2) + NT - 1) / NT;   /* K pairs */
+        constexpr int VI = (TL_DEC_MAX_NEW * (D / 8) + NT - 1) / NT;   /* V 8-element units */
+        const u32 pairs = p.rope.rdim >> 1;
+        const u32 nkp = need_new ? p.rows_per_seq * (D / 2) : 0u;
+        const u32 nvu = need_new ? p.rows_per_seq * VPR : 0u;
+        /* element indices of pair i: rotated pairs per the RoPE variant,
+         * the rest (i >= pairs) stay adjacent */
+        auto pair_of = [&](u32 i, u32 &ia, u32 &ib) {
+            const bool rot = i < pairs;
+            ia = (rot && p.rope.neox) ? i : 2 * i;
+            ib = (rot && p.rope.neox) ? i + pairs : 2 * i + 1;
+        };
+        float qx[QI], qy[QI], kx[KI], ky[KI];
+        float4 va[VI], vc[VI];
+#pragma unroll
+        for (int j = 0; j < QI; j++) {
+            const u32 t = tid + j * NT;
+            qx[j] = qy[j] = 0.f;
+            if (t < (u32)G * (D / 2)) {
+                u32 ia, ib;
+                pair_of(t % (D / 2), ia, ib);
+                const float *row = qb + (t / (D / 2)) * D;
+                qx[j] = row[ia];
+                qy[j] = row[ib];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KI; j++) {
+            const u32 t = tid + j * NT;
+            kx[j] = ky[j] = 0.f;
+            if (t < nkp) {
+                u32 ia, ib;
+                pair_of(t % (D / 2), ia, ib);
+                const float *src = sq.kin + (u64)(t / (D / 2)) * sq.kv_stride + (u64)kvh * D;
+                kx[j] = src[ia];
+                ky[j] = src[ib];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < VI; j++) {
+            const u32 i = tid + j * NT;
+            va[j] = vc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < nvu) {
+                const float *src = sq.vin + (u64)(i / VPR) * sq.kv_stride + (u64)kvh * D + (i % VPR) * 8;
+                va[j] = *(const float4 *)src;
+                vc[j] = *(const float4 *)(src + 4);
+            }
+        }
+        /* the rotation (powf + sincosf per pair, ~1 us per thread) runs
+         * while the first tiles are in flight: the loaded values are pinned
+         * here (the compiler waits for them now, not behind the tile
+         * loads), then the slots are staged, the tiles issued, and q and
+         * the new rows rotated, converted and stored */
+#pragma unroll
+        for (int j = 0; j < QI; j++) __asm__ volatile("" : "+v"(qx[j]), "+v"(qy[j]));
+#pragma unroll
+        for (int j = 0; j < KI; j++) __asm__ volatile("" : "+v"(kx[j]), "+v"(ky[j]));
+#pragma unroll
+        for (int j = 0; j < VI; j++)
+            __asm__ volatile("" : "+v"(va[j].x), "+v"(va[j].y), "+v"(va[j].z), "+v"(va[j].w),
+                             "+v"(vc[j].x), "+v"(vc[j].y), "+v"(vc[j].z), "+v"(vc[j].w));
+        stage_and_issue();
+        u16 *q16 = (u16 *)s_q;
+#pragma unroll
+        for (int j = 0; j < QI; j++) {
+            const u32 t = tid + j * NT;
+            if (t < (u32)G * (D / 2)) {
+                const u32 h = t / (D / 2), i = t % (D / 2);
+                u32 ia, ib;
+                pair_of(i, ia, ib);
+                float x = qx[j], y = qy[j];
+                if (i < pairs) {
+                    float c, sn;
+                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
+                    rope_rot(qx[j], qy[j], c, sn, x, y);
+                }
+                const u32 pk = pack_f16x2_fast(x * sc, y * sc);
+                q16[h * D + ia] = (u16)(pk & 0xffffu);
+                q16[h * D + ib] = (u16)(pk >> 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KI; j++) {
+            const u32 t = tid + j * NT;
+            if (t < nkp) {
+                const u32 row = t / (D / 2), i = t % (D / 2);
+                u32 ia, ib;
+                pair_of(i, ia, ib);
+                float x = kx[j], y = ky[j];
+                if (i < pairs) {
+                    float c, sn;
+                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + row, c, sn);
+                    rope_rot(kx[j], ky[j], c, sn, x, y);
+                }
+                u16 *k16 = (u16 *)s_newk[row];
+                k16[ia] = (u16)f32_to_f16_bits(x);
+                k16[ib] = (u16)f32_to_f16_bits(y);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < VI; j++) {
+            const u32 i = tid + j * NT;
+            if (i < nvu) s_newv[i / VPR][i % VPR] = cvt8_f16_regs(va[j], vc[j]);
+        }
+        __syncthreads();   /* q and the new rows */
+    } else {
+        /* one q item and at most one new-row item per thread (G * D / 8 and
+         * TL_DEC_MAX_NEW * D / 8 are at most NT): all loads first */
+        static_assert(G * D / 8 <= NT && TL_DEC_MAX_NEW * (D / 8) <= NT, "one item per thread");
+        float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qc = qa;
+        float4 ka = qa, kc = qa, va = qa, vc = qa;
+        const bool has_q = tid < G * D / 8;
+        const bool has_new = need_new && (u32)tid < p.rows_per_seq * VPR;
+        const u32 nrow = (u32)tid / VPR, nc8 = (u32)tid % VPR;
+        if (has_q) {
+            qa = *(const float4 *)(qb + tid * 8);
+            qc = *(const float4 *)(qb + tid * 8 + 4);
+        }
+        if (has_new) {
+            const u64 src = (u64)nrow * sq.kv_stride + (u64)kvh * D + nc8 * 8;
+            ka = *(const float4 *)(sq.kin + src);
+            kc = *(const float4 *)(sq.kin + src + 4);
+            va = *(const float4 *)(sq.vin + src);
+            vc = *(const float4 *)(sq.vin + src + 4);
+        }
+        if (has_q)
+            s_q[tid] = make_uint4(pack_f16x2_fast(qa.x * sc, qa.y * sc), pack_f16x2_fast(qa.z * sc, qa.w * sc),
+                                  pack_f16x2_fast(qc.x * sc, qc.y * sc), pack_f16x2_fast(qc.z * sc, qc.w * sc));
+        if (has_new) {
+            s_newk[nrow][nc8] = cvt8_f16_regs(ka, kc);
+            s_newv[nrow][nc8] = cvt8_f16_regs(va, vc);
+        }
+    }
+    if constexpr (!ROPE) stage_and_issue();
+
 
     /* q of this lane's 16 dims, every head of the group */
     u32 qr[G][8];
