@@ -28,6 +28,7 @@ One JSON line is printed; besides the contract fields:
   prefill, append, hbm_read_ceiling   the other measured rows
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -848,6 +849,22 @@ def main():
     del ck, cv, cq, co
     app_tok_s = n_chunks * ub / (app_ms / 1e3)
     app_bytes = n_chunks * ub * L * kd * 2 * (4 + 2)
+    # the same chunks written through all layers per call (tl_kv_append_layers,
+    # the session's write-through: launches of 16 layers), rows rewritten with
+    # new values at the same positions
+    bk = torch.randn((L, ub, kd), generator=gen, device="cuda")
+    bv = torch.randn((L, ub, kd), generator=gen, device="cuda")
+    arr = (tlkv.KvLayer * L)(*[x.desc for x in layers])
+    kp = (ctypes.c_void_p * L)(*[bk[l].data_ptr() for l in range(L)])
+    vp_ = (ctypes.c_void_p * L)(*[bv[l].data_ptr() for l in range(L)])
+    torch.cuda.synchronize()
+    e[0].record(stream)
+    for ci in range(n_chunks):
+        tlkv.check(lib.tl_kv_append_layers(arr, L, kp, vp_, kd, tlkv.ptr(slots), ci * ub, ub, sh))
+    e[1].record(stream)
+    torch.cuda.synchronize()
+    appl_ms = e[0].elapsed_time(e[1])
+    del bk, bv
 
     # ---- 3. decode ---------------------------------------------------------
     q = torch.randn((L, 1, qd), generator=gen, device="cuda")
@@ -1025,6 +1042,11 @@ def main():
         "decode_with_rope_us_per_layer": {**rope_us, "steps": rope_steps,
                                           "note": "RoPE on q and the new k row each step: "
                                                   "tl_rope x2 + tl_attn vs tl_attn_rope"},
+        "append_layers": {"tok_s": round(n_chunks * ub / (appl_ms / 1e3), 1),
+                          "GBs": round(app_bytes / (appl_ms / 1e3) / 1e9, 1),
+                          "note": "the same 64 x 512-row chunks, each written through all 32 "
+                                  "layers by one tl_kv_append_layers call (launches of 16 "
+                                  "layers), as the session's write-through does"},
         "append": {"tok_s": round(app_tok_s, 1), "GBs": round(app_bytes / (app_ms / 1e3) / 1e9, 1),
                    "note": "64 x 512-row tl_kv_append per layer; a token counts once "
                            "for all 32 layers; decode appends are fused into the decode "
