@@ -976,6 +976,43 @@ def main():
                                "the slot-table reads"}
     del perm
 
+    # several batch rows of one session per OP_ATTN (a multi-token decode
+    # step: speculative or draft tokens): the matrix-core tile folds the
+    # rows of a group into its MFMA columns, so the K/V bytes are read once
+    # for all of them; timed against one row per workgroup group
+    # (TL_TUNE_DECODE_ROWS = 1), on rows already in the cache (no append)
+    mr_n, mr_steps = 4, min(64, K)
+    q4 = torch.randn((mr_n, qd), generator=gen, device="cuda")
+    o4 = torch.empty((mr_n, qd), dtype=torch.float32, device="cuda")
+    a4 = [tlkv.attn_args(q4, None, None, o4, None, pos - mr_n, mr_n, Hq, d, Hkv, 0, scale)
+          for l in range(L)]
+    mr_us = {}
+    for rows in (0, 1):
+        with tlkv.tuning(tlkv.TUNE_DECODE_ROWS, rows):
+            for l in range(L):
+                tlkv.check(noapp(descs[l], a4[l], sh))
+            torch.cuda.synchronize()
+            e0, e1 = ev(), ev()
+            e0.record(stream)
+            for _ in range(mr_steps):
+                for l in range(L):
+                    rc = noapp(descs[l], a4[l], sh)
+                    if rc:
+                        tlkv.check(rc)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        mr_us["folded" if rows == 0 else "row_per_group"] = e0.elapsed_time(e1) * 1e3 / (mr_steps * L)
+    mr_bytes = cont_bytes + (mr_n - 1) * Hq * d * 8     # K/V once; q and out per row
+    decode_multi_row = {"rows": mr_n,
+                        "us_per_layer_launch": {k_: round(v_, 3) for k_, v_ in mr_us.items()},
+                        "GBs_folded": round(mr_bytes / (mr_us["folded"] * 1e-6) / 1e9, 1),
+                        "steps": mr_steps,
+                        "note": f"OP_ATTN of {mr_n} batch rows of one session at P = {pos} "
+                                "keys (contiguous cache, no append): the rows folded into one "
+                                "matrix-core group (K/V read once) vs one row per group "
+                                "(TL_DECODE_ROWS=1); GBs_folded counts K/V once"}
+    del q4, o4
+
     # decode step with RoPE on q and the new k row (the reference's OP_ROPE x2
     # + OP_ATTN): three launches per layer (tl_rope, tl_rope, tl_attn) vs one
     # (tl_attn_rope), on raw (un-rotated) q/k rows; cache rows written past
@@ -1039,6 +1076,7 @@ def main():
                    "frac_of_measured_ceiling": round(value / ceiling, 4)},
         "decode_contiguous": decode_contiguous,
         "decode_permuted_slots": decode_permuted,
+        "decode_multi_row": decode_multi_row,
         "decode_with_rope_us_per_layer": {**rope_us, "steps": rope_steps,
                                           "note": "RoPE on q and the new k row each step: "
                                                   "tl_rope x2 + tl_attn vs tl_attn_rope"},

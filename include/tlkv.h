@@ -126,7 +126,8 @@ int tl_init(int device);
 #define TL_TUNE_PREFILL_APPEND_POLLS 7  /* n: at most n - 1 polls per wait for the fused append */
 #define TL_TUNE_PREFILL_SEPARATE_APPEND 8 /* 1: prefill batches append in a launch of their own */
 #define TL_TUNE_DECODE_MFMA         9   /* 1: decode tiles on the vector ALUs, 2: on the matrix cores */
-#define TL_TUNE_COUNT               10
+#define TL_TUNE_DECODE_ROWS        10   /* n: batch rows per matrix-core decode group (1: one) */
+#define TL_TUNE_COUNT               11
 int tl_set_tuning(int key, uint32_t value);
 uint32_t tl_get_tuning(int key);
 

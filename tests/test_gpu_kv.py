@@ -367,6 +367,41 @@ def test_decode_variants_agree(T, shape):
         assert np.abs(outs[0] - o).max() < 1e-4
 
 
+FOLD_CASES = [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted slots, ring
+    (32, 8, 128, 8300, 8000, 4, 0, False, 0),   # config 4 shape: 4 rows per group, splits
+    (28, 4, 128, 3000, 2900, 7, 0, True, 0),    # gqa 7: 2 rows per group, ragged last block
+    (8, 8, 64, 1300, 1000, 15, 0, True, 0),     # MHA: 15 rows in one group
+    (16, 2, 64, 2100, 2000, 15, 0, False, 0),   # gqa 8, head_dim 64
+    (8, 4, 256, 2100, 1800, 9, 1024, True, 0),  # head_dim 256, windowed, ragged
+    (16, 4, 128, 0, 600, 6, 200, False, 210),   # ring of a windowed layer
+    (32, 8, 128, 600, 0, 15, 0, True, 0),       # from an empty cache
+    (32, 8, 128, 33000, 32000, 4, 0, False, 0), # 32K keys
+]
+
+
+@pytest.mark.parametrize("case", FOLD_CASES)
+def test_decode_row_folding(T, case):
+    """Several batch rows of a session in one matrix-core group (their heads
+    side by side as MFMA columns, each column masked to its own row's keys):
+    within tolerance of the oracle, and of the one-row-per-group launch up
+    to rounding."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n, window, perm, ring = case
+    cap = ring or cap
+    rng = np.random.default_rng(cap + pos + n)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    outs = []
+    for rows in (0, 1):
+        with tlkv.tuning(tlkv.TUNE_DECODE_MFMA, 2), tlkv.tuning(tlkv.TUNE_DECODE_ROWS, rows):
+            out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                            seed=pos + n, ring=ring)
+        assert np.abs(out - o16).max() < TOL, (case, rows)
+        assert np.abs(out - o32).max() < TOL, (case, rows)
+        outs.append(out)
+    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+
+
 def test_decode_batch_sessions(T):
     """Multi-session one-token decode equals per-session OP_ATTN."""
     import tlkv

@@ -222,6 +222,31 @@ def test_attn_q8_decode_tile_paths(T, case, tile):
     assert np.abs(out - ref).max() < TOL
 
 
+@pytest.mark.parametrize("case", [
+    # n_head, n_kv, hd, cap, pos, n, window, permuted slots, ring
+    (40, 5, 128, 3000, 2900, 6, 0, True, 0),      # gqa 8: 2 rows per group
+    (16, 4, 64, 2000, 1900, 7, 0, False, 0),      # gqa 4, head_dim 64: 4 rows, ragged
+    (8, 8, 64, 1200, 1000, 15, 0, True, 0),       # MHA: 15 rows in one group
+    (8, 4, 256, 2100, 1800, 9, 1024, True, 0),    # head_dim 256, windowed
+    (32, 8, 128, 8300, 8000, 4, 0, False, 0),     # splits
+])
+def test_attn_q8_row_folding(T, case):
+    """Batch rows folded into one matrix-core group over the Q8_0 cache:
+    within tolerance of the Q8_0 oracle with and without folding."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n, window, perm, ring = case
+    rng = np.random.default_rng(pos + 7 * n)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    outs = []
+    for rows in (0, 1):
+        with tlkv.tuning(tlkv.TUNE_DECODE_MFMA, 2), tlkv.tuning(tlkv.TUNE_DECODE_ROWS, rows):
+            out, ref, _, _ = _run_attn_q8(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                          seed=pos + n, ring=ring)
+        assert np.abs(out - ref).max() < TOL, (case, rows)
+        outs.append(out)
+    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+
+
 @pytest.mark.parametrize("n", [1, 4, 40])
 def test_attn_noappend_q8(T, n):
     rng = np.random.default_rng(n)

@@ -41,6 +41,7 @@ CASES = [
     (28, 4, 128, 900, 1, 128, 1, 1e6),       # decode, NEOX, gqa 7 (configs 2, 3)
     (8, 4, 256, 1500, 1, 256, 1, 1e4),       # decode, head_dim 256 (config 5)
     (16, 2, 128, 300, 5, 64, 1, 1e4),        # multi-row decode, partial rope_dim
+    (32, 8, 128, 2000, 6, 128, 0, 5e5),      # multi-row decode, 4 rows per group, ragged
     (32, 8, 128, 1000, 100, 128, 0, 5e5),    # prefill batch (append + MFMA kernel)
     (8, 4, 64, 200, 40, 32, 0, 1e4),         # prefill, head_dim 64, partial NORM
     (32, 8, 64, 700, 1, 64, 0, 5e5),         # decode, head_dim 64 (config 1 shape)

@@ -113,8 +113,8 @@ static int resident_per_cu(const void *fn, int threads) {
  * gets the same number of equal key chunks).  The partials of a split group
  * are merged by the group's last workgroup when they fit its LDS, else by
  * attn_merge_kernel. */
-int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
-                     u32 max_vis, hipStream_t st, bool q8) {
+static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u32 max_vis,
+                         hipStream_t st, bool q8, bool fold_rows) {
     if (q8) {
         for (u32 i = 0; i < TL_MAX_BATCH_SEQ; i++)
             if (p.seq[i].kin) return tl_fail(TL_EINVAL, "decode: no fused append into a Q8_0 cache");
@@ -144,7 +144,21 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     int per_cu = resident_per_cu(K.fn, K.threads);
     if (per_cu > 2) per_cu = 2;
     const u32 target = tuned(TL_TUNE_DECODE_WGS, (u32)(per_cu * cu_count()));
-    const u64 n_groups = (u64)n_rows_total * p.n_kv;
+    /* matrix-core tile: R batch rows of a session share each workgroup
+     * group (their heads side by side as MFMA columns, R x gqa <= 16, 8 at
+     * head_dim 256), so the rows read each K/V byte once instead of R
+     * times; their partials are merged inside the launch */
+    const u32 rows = p.rows_per_seq ? p.rows_per_seq : 1u;
+    u32 R = 1;
+    if (fold_rows && mf && rows > 1 && !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL)) {
+        const u32 most = (head_dim == 256 ? 8u : 16u) / G;
+        R = tuned(TL_TUNE_DECODE_ROWS, most);
+        if (R > most) R = most;
+        if (R > rows) R = rows;
+        if (R < 1) R = 1;
+    }
+    if (R > 1 && p.window) max_vis += R - 1;   /* the rows' windows start apart */
+    u64 n_groups = (u64)(n_rows_total / rows) * ((rows + R - 1) / R) * p.n_kv;
     u32 n_split = (u32)((target + n_groups - 1) / n_groups);
     const u32 waves = (u32)K.threads / 64;
     /* fewest keys per split: a tile for every wave at head_dim 128, for half
@@ -168,9 +182,15 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     p.n_split = n_split;
     p.counters = nullptr;
     p.dist = 0;
-    const bool in_kernel_merge = n_split > 1 && G * n_split <= 2048 &&
+    const bool in_kernel_merge = n_split > 1 && R * G * n_split <= 2048 &&
                                  n_groups <= TL_MERGE_MAX_GROUPS &&
                                  !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL);
+    if (R > 1 && n_split > 1 && !in_kernel_merge) {
+        /* the separate merge launch reads one row per group: plan again */
+        if (p.window) max_vis -= R - 1;
+        return launch_decode(p, n_rows_total, head_dim, G, max_vis, st, q8, false);
+    }
+    p.rows_per_wg = R;
     if (n_split > 1) {
         /* every split merges a slice of the output (dist) when there are
          * enough splits to share the merge (measured: with 8 or fewer the
@@ -180,7 +200,7 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
         p.dist = in_kernel_merge && n_split >= 12 && n_split <= TL_MERGE_MAX_SPLIT_DIST &&
                  (u64)n_split * n_groups <= resident && !tl_tune(TL_TUNE_DECODE_SINGLE_MERGE);
         TlWorkspace *w;
-        size_t parts = (size_t)n_rows_total * p.n_head * n_split;
+        size_t parts = (size_t)n_groups * R * G * n_split;
         /* dist: one (m, l, epoch, ~epoch) record of 16 bytes per partial */
         int rc = tl_workspace_get(st, parts * head_dim, p.dist ? 2 * parts : parts,
                                   in_kernel_merge ? TL_MERGE_CNT_WORDS : 0, &w);
@@ -197,6 +217,11 @@ int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
     HIP_TRY(hipLaunchKernel(K.fn, dim3(n_split * (u32)n_groups), dim3(K.threads), args, 0, st));
     if (n_split == 1 || in_kernel_merge) return TL_OK;
     return tl_launch_merge(p, n_rows_total, head_dim, st);
+}
+
+int tl_launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G,
+                     u32 max_vis, hipStream_t st, bool q8) {
+    return launch_decode(p, n_rows_total, head_dim, G, max_vis, st, q8, true);
 }
 
 int tl_launch_merge(const DecParams &p, u32 n_rows_total, u32 head_dim, hipStream_t st) {

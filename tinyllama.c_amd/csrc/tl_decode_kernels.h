@@ -427,22 +427,40 @@ TL_DEV dh4_t ld_tr16_h4(const _Float16 *lds_ptr) {
 /* Mask, online softmax and PV of one tile's score blocks s (keys
  * tbase + 16b + 4*(lane/16) + i of head lane & 15) against the f16 V tile tv
  * (row t, chunk c at unit t*CPR + (c ^ (t & 1))). */
+/* Column masks when a group holds several batch rows: column lane & 15 sees
+ * the keys [klo, khi) of its own row; the rows' ranges differ only below
+ * ulo (their window starts) and from uhi on (their ends), so tiles inside
+ * [ulo, uhi) need no column mask. */
+struct MfRows {
+    u32 klo, khi;   /* this lane's column */
+    u32 ulo, uhi;   /* keys every row of the group sees */
+    bool multi;     /* more than one row */
+};
+
 template <int D, int G>
 TL_DEV void mf_softmax_pv(df4_t (&s)[(RCfg<D>::TK + 15) / 16], const uint4 *tv, u32 tbase,
-                          u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+                          u32 kend, const MfRows &mr, int lane, float &m, float &l,
+                          df4_t (&O)[D / 16]) {
     using C = RCfg<D>;
     constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, DB = D / 16;
     constexpr float NEG_INF = -__builtin_huge_valf();
     const int g = lane >> 4, c = lane & 15;
-    /* keys past the chunk (wave-uniform: only a chunk's last tile) and the
-     * copied rows of 8-key tiles */
-    if (TK < 16 || tbase + (u32)TK > kend) {
+    /* keys past the chunk (wave-uniform: only a chunk's last tile), the
+     * copied rows of 8-key tiles, and keys outside a column's own row */
+    const bool cols = mr.multi && (tbase < mr.ulo || tbase + (u32)TK > mr.uhi);
+    if (TK < 16 || tbase + (u32)TK > kend || cols) {
+        /* the lane's visible keys [lo, hi) as one unsigned range test
+         * (key - lo < n); a select per element, no branch */
+        const u32 lo = cols ? mr.klo : 0u;
+        const u32 hi = cols ? min(mr.khi, kend) : kend;
+        const u32 n = hi > lo ? hi - lo : 0u;
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const u32 kk = (u32)(16 * b + 4 * g + i);
-                if (kk >= (u32)TK || tbase + kk >= kend) s[b][i] = NEG_INF;
+                const bool live = kk < (u32)TK && tbase + kk - lo < n;
+                s[b][i] = live ? s[b][i] : NEG_INF;
             }
     }
     float mx = NEG_INF;
@@ -488,7 +506,8 @@ TL_DEV void mf_softmax_pv(df4_t (&s)[(RCfg<D>::TK + 15) / 16], const uint4 *tv, 
 
 template <int D, int G>
 TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32], u32 tbase,
-                      u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+                      u32 kend, const MfRows &mr, int lane, float &m, float &l,
+                      df4_t (&O)[D / 16]) {
     using C = RCfg<D>;
     constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32;
     const int g = lane >> 4, c = lane & 15;
@@ -503,7 +522,7 @@ TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32
                                                          qb[j], acc, 0, 0, 0);
         s[b] = acc;
     }
-    mf_softmax_pv<D, G>(s, tv, tbase, kend, lane, m, l, O);
+    mf_softmax_pv<D, G>(s, tv, tbase, kend, mr, lane, m, l, O);
 }
 
 /* mfma_tile over a Q8_0 tile (int8 rows as loaded: row t at byte t*D; f16
@@ -518,7 +537,8 @@ TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32
  * precede the overwrite. */
 template <int D, int G>
 TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t (&qb)[D / 32],
-                         u32 tbase, u32 kend, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
+                         u32 tbase, u32 kend, const MfRows &mr, int lane, float &m, float &l,
+                         df4_t (&O)[D / 16]) {
     using C = RCfg<D>;
     constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32, NSB = D / 32;
     constexpr int VU = TK * CPR / 64;              /* 8-byte V units per lane */
@@ -583,7 +603,7 @@ TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t
         stage[t * CPR + (cc ^ (t & 1))] = q8_dequant8(vw[k], (u32)vsc[k]);
     }
     __builtin_amdgcn_wave_barrier();
-    mf_softmax_pv<D, G>(s, stage, tbase, kend, lane, m, l, O);
+    mf_softmax_pv<D, G>(s, stage, tbase, kend, mr, lane, m, l, O);
 }
 
 constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 : x >= 2 ? 2 : 1; }
@@ -595,11 +615,12 @@ constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 
  * batch of partial rows and every (m, l) pair are requested together
  * (device-coherent loads); the pairs go through LDS (s_ml: G*n_split). */
 template <int D, int G, int NT>
-TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const DecSeq &sq,
-                             float2 *s_ml) {
+TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, u32 gh, u32 ncol,
+                             const DecSeq &sq, float2 *s_ml) {
     constexpr float NEG_INF = -__builtin_huge_valf();
-    constexpr int COLS = G * D / 4;
-    constexpr int TPC = pow2_floor(NT / COLS > 16 ? 16 : (NT / COLS < 1 ? 1 : NT / COLS));
+    constexpr int COLS_MAX = G * D / 4;
+    const int COLS = (int)ncol * (D / 4);
+    constexpr int TPC = pow2_floor(NT / COLS_MAX > 16 ? 16 : (NT / COLS_MAX < 1 ? 1 : NT / COLS_MAX));
     constexpr int K = 8;                       /* splits per load batch */
     const int tid = threadIdx.x;
     const u32 ns = p.n_split;
@@ -618,7 +639,7 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
         }
     };
     if (col0 < COLS) load_batch(col0, (u32)part);
-    for (u32 i = tid; i < (u32)G * ns; i += NT) {
+    for (u32 i = tid; i < ncol * ns; i += NT) {
         const u32x2v_t ml = __builtin_amdgcn_raw_buffer_load_b64(rml, i * 8, 0, TL_SC1);
         s_ml[i] = make_float2(__uint_as_float(ml[0]), __uint_as_float(ml[1]));
     }
@@ -668,7 +689,7 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
         }
         if (part == 0) {
             const float inv = 1.0f / L;
-            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)(kvh * G + h) * D + d] =
+            *(float4 *)&sq.dst[(u64)(r + h / gh) * p.q_stride + (u64)(kvh * gh + h % gh) * D + d] =
                 make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
         }
     }
@@ -685,11 +706,11 @@ TL_DEV void split_merge_regs(const DecParams &p, u32 pb, u32 kvh, u32 r, const D
  * holding split s (n_split <= 64): out = sum_s w_s acc_s / sum_s w_s l_s,
  * w_s = exp2(m_s - max m).  Partial rows and their (m, l, epoch) records
  * (float4 per partial) are read with device-coherent loads. */
-template <int D, int G, int W>
-TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq &sq,
-                        u32 slice, u32 cps) {
+template <int D, int W>
+TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, u32 gh, u32 ncol,
+                        const DecSeq &sq, u32 slice, u32 cps) {
     constexpr float NEG_INF = -__builtin_huge_valf();
-    constexpr u32 COLS = G * D / 4;
+    const u32 COLS = ncol * (D / 4);
     const u32 ns = p.n_split;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const u32 c0 = slice * cps, c1 = min(c0 + cps, COLS);
@@ -716,7 +737,7 @@ TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, const DecSeq
         const float oz = group_sum<64>(w * a.z), ow = group_sum<64>(w * a.w);
         if (lane == 0) {
             const float inv = 1.0f / L;
-            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)(kvh * G + h) * D + d] =
+            *(float4 *)&sq.dst[(u64)(r + h / gh) * p.q_stride + (u64)(kvh * gh + h % gh) * D + d] =
                 make_float4(ox * inv, oy * inv, oz * inv, ow * inv);
         }
     }
@@ -752,8 +773,13 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     __shared__ uint4 s_ring[W][RING_U];          /* per wave: S stages of (K, V) */
     __shared__ u32 s_scl[Q8 ? W : 1][Q8 ? S * 64 : 1];
     __shared__ u32 s_slot[TL_DEC_MAX_CHUNK];
-    __shared__ uint4 s_q[G * D / 8];
-    __shared__ float s_m[W][G];
+    /* columns of the group's state: the G heads of one row, or with the
+     * matrix-core tile up to 16 (8 at head_dim 256, for LDS) = (batch rows
+     * of the group) x G */
+    constexpr int CGT = MF ? (D == 256 ? 8 : 16) : G;
+    static_assert(CGT >= G, "a row's heads fit the columns");
+    __shared__ uint4 s_q[CGT * D / 8];
+    __shared__ float s_m[W][CGT];
     __shared__ uint4 s_newk[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
     __shared__ uint4 s_newv[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
 
@@ -779,14 +805,22 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         grp = bid / n_split;
         split = bid % n_split;
     }
+    /* group = (session, block of R batch rows, kv-head); R > 1 only with the
+     * matrix-core tile.  The group's keys run from its first row's window
+     * start to its last row's last key; each column masks its own row's. */
+    const u32 R = MF && p.rows_per_wg > 1 ? p.rows_per_wg : 1u;
+    const u32 RB = (p.rows_per_seq + R - 1) / R;
     const u32 kvh = grp % p.n_kv;
-    const u32 grow = grp / p.n_kv;
-    const u32 si = grow / p.rows_per_seq;
-    const u32 r = grow % p.rows_per_seq;
+    const u32 gblk = grp / p.n_kv;
+    const u32 si = gblk / RB;
+    const u32 r = (gblk % RB) * R;                    /* the group's first row */
+    const u32 nr = min(R, p.rows_per_seq - r);        /* its rows */
+    const u32 cg = MF ? nr * G : (u32)G;              /* its columns */
     const DecSeq sq = p.seq[si];
 
-    const u32 n_keys = sq.pos + r + 1;
-    const u32 start = (p.window && n_keys > p.window) ? n_keys - p.window : 0;
+    const u32 n_keys = sq.pos + r + nr;
+    const u32 n_keys0 = sq.pos + r + 1;
+    const u32 start = (p.window && n_keys0 > p.window) ? n_keys0 - p.window : 0;
     const u32 kbeg = start + split * p.chunk;
     const u32 kend = min(kbeg + p.chunk, n_keys);
     const bool fused = !Q8 && sq.kin != nullptr;
@@ -890,7 +924,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         /* pairs (ia, ib) of q and of the new K rows, rotated by position,
          * and the new V rows: every thread requests its (few) items first,
          * then rotates, converts and stores them */
-        constexpr int QI = (G * (D / 2) + NT - 1) / NT;                /* q pairs */
+        constexpr int QI = (CGT * (D / 2) + NT - 1) / NT;              /* q pairs */
         constexpr int KI = (TL_DEC_MAX_NEW * (D / 2) + NT - 1) / NT;   /* K pairs */
         constexpr int VI = (TL_DEC_MAX_NEW * (D / 8) + NT - 1) / NT;   /* V 8-element units */
         const u32 pairs = p.rope.rdim >> 1;
@@ -909,10 +943,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         for (int j = 0; j < QI; j++) {
             const u32 t = tid + j * NT;
             qx[j] = qy[j] = 0.f;
-            if (t < (u32)G * (D / 2)) {
+            if (t < cg * (D / 2)) {
                 u32 ia, ib;
                 pair_of(t % (D / 2), ia, ib);
-                const float *row = qb + (t / (D / 2)) * D;
+                /* column t / (D/2) = batch row (of the group) x G + head */
+                const u32 col = t / (D / 2);
+                const float *row = qb + (u64)(col / G) * p.q_stride + (col % G) * D;
                 qx[j] = row[ia];
                 qy[j] = row[ib];
             }
@@ -957,14 +993,14 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 #pragma unroll
         for (int j = 0; j < QI; j++) {
             const u32 t = tid + j * NT;
-            if (t < (u32)G * (D / 2)) {
+            if (t < cg * (D / 2)) {
                 const u32 h = t / (D / 2), i = t % (D / 2);
                 u32 ia, ib;
                 pair_of(i, ia, ib);
                 float x = qx[j], y = qy[j];
                 if (i < pairs) {
                     float c, sn;
-                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r, c, sn);
+                    rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + r + h / G, c, sn);
                     rope_rot(qx[j], qy[j], c, sn, x, y);
                 }
                 const u32 pk = pack_f16x2_fast(x * sc, y * sc);
@@ -999,15 +1035,17 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     } else {
         /* one q item and at most one new-row item per thread (G * D / 8 and
          * TL_DEC_MAX_NEW * D / 8 are at most NT): all loads first */
-        static_assert(G * D / 8 <= NT && TL_DEC_MAX_NEW * (D / 8) <= NT, "one item per thread");
+        static_assert(CGT * D / 8 <= NT && TL_DEC_MAX_NEW * (D / 8) <= NT, "one item per thread");
         float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qc = qa;
         float4 ka = qa, kc = qa, va = qa, vc = qa;
-        const bool has_q = tid < G * D / 8;
+        const bool has_q = (u32)tid < cg * (D / 8);
+        /* column tid / (D/8) = batch row (of the group) x G + head */
+        const float *qrow = qb + (u64)((u32)tid / (G * D / 8)) * p.q_stride + ((u32)tid % (G * D / 8)) * 8;
         const bool has_new = need_new && (u32)tid < p.rows_per_seq * VPR;
         const u32 nrow = (u32)tid / VPR, nc8 = (u32)tid % VPR;
         if (has_q) {
-            qa = *(const float4 *)(qb + tid * 8);
-            qc = *(const float4 *)(qb + tid * 8 + 4);
+            qa = *(const float4 *)qrow;
+            qc = *(const float4 *)(qrow + 4);
         }
         if (has_new) {
             const u64 src = (u64)nrow * sq.kv_stride + (u64)kvh * D + nc8 * 8;
@@ -1051,10 +1089,23 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     dh8_t qm[MF ? D / 32 : 1];
     df4_t O1[MF ? D / 16 : 1];
     float m1 = NEG_INF, l1 = 0.f;
+    MfRows mr = {0u, 0xffffffffu, 0u, 0xffffffffu, false};
     if constexpr (MF) {
         const int c = lane & 15, g = lane >> 4;
+        if (nr > 1) {
+            /* per-column key ranges of the group's rows (columns past the
+             * group's rows see everything: their q is zero) */
+            auto row_start = [&](u32 n) { return (p.window && n > p.window) ? n - p.window : 0u; };
+            mr.multi = true;
+            mr.ulo = row_start(n_keys);      /* the last row's window start */
+            mr.uhi = n_keys0;                /* the first row's end */
+            if ((u32)c < cg) {
+                mr.khi = sq.pos + r + (u32)c / G + 1;
+                mr.klo = row_start(mr.khi);
+            }
+        }
 #pragma unroll
-        for (int j = 0; j < D / 32; j++) qm[j] = c < G ? u4_as_h8(s_q[c * CPR + 4 * j + g]) : dh8_t{};
+        for (int j = 0; j < D / 32; j++) qm[j] = (u32)c < cg ? u4_as_h8(s_q[c * CPR + 4 * j + g]) : dh8_t{};
 #pragma unroll
         for (int db = 0; db < D / 16; db++) O1[db] = df4_t{0.f, 0.f, 0.f, 0.f};
     }
@@ -1090,12 +1141,13 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
             if constexpr (MF)
                 mfma_tile_q8<D, G>(&s_ring[wave][(j % S) * STAGE_U], ss, ss + 64, qm,
-                                   kbeg + (wave + W * j) * TK, kend, lane, m1, l1, O1);
+                                   kbeg + (wave + W * j) * TK, kend, mr, lane, m1, l1, O1);
             else
                 ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
                                    kend, lane, m, l, acc);
         } else if constexpr (MF) {
-            mfma_tile<D, G>(st, st + UNITS, qm, kbeg + (wave + W * j) * TK, kend, lane, m1, l1, O1);
+            mfma_tile<D, G>(st, st + UNITS, qm, kbeg + (wave + W * j) * TK, kend, mr, lane, m1,
+                            l1, O1);
         } else {
             ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
         }
@@ -1116,15 +1168,18 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     /* ---- one state per workgroup and head, then its output or partial ---- */
     const bool single = (n_split == 1);
     const bool last_merges = p.counters != nullptr;
-    const u32 pb = (grow * p.n_head + kvh * G) * n_split;
-    __shared__ float2 s_rec[G];
-    /* output float4 (head h, dims d..d+3) of the workgroup's state: the
-     * result itself (one split) or the split's partial */
+    /* the group's partials: [column][split][D] from pb (R = 1: the layout
+     * attn_merge_kernel reads, [row][head][split][D]) */
+    const u32 pb = grp * (R * G) * n_split;
+    __shared__ float2 s_rec[CGT];
+    /* output float4 (column h = batch row of the group x G + head, dims
+     * d..d+3) of the workgroup's state: the result itself (one split) or
+     * the split's partial */
     auto emit = [&](int h, int d, float mm, float L, float4 O) __attribute__((always_inline)) {
-        const u32 hq = kvh * G + h;
+        const u32 hq = kvh * G + (u32)h % G, row = r + (u32)h / G;
         if (single) {
             const float inv = 1.0f / L;
-            *(float4 *)&sq.dst[(u64)r * p.q_stride + (u64)hq * D + d] =
+            *(float4 *)&sq.dst[(u64)row * p.q_stride + (u64)hq * D + d] =
                 make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
         } else if (last_merges) {
             /* device-coherent stores: the merging workgroup may run
@@ -1143,24 +1198,24 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                         buf_rsrc(p.ws_ml + pb), pi * 8, 0, TL_SC1);
             }
         } else {
-            const u64 pi = ((u64)grow * p.n_head + hq) * n_split + split;
+            const u64 pi = ((u64)gblk * p.n_head + hq) * n_split + split;
             *(float4 *)&p.ws_acc[pi * D + d] = O;
             if (d == 0) p.ws_ml[pi] = make_float2(mm, L);
         }
     };
     if constexpr (MF) {
         /* a column's sum over its four lanes; then every wave writes its
-         * heads' (m, l) and O^T rows into its own ring region (no barrier:
+         * columns' (m, l) and O^T rows into its own ring region (no barrier:
          * that region is no longer read), and after one barrier thread
          * (h, d4) combines the waves with weights exp2(m_w - M_h) */
-        __shared__ float s_lw[MF ? G : 1][W];
-        static_assert(G <= 16 && G * D / 4 <= NT, "one head column per lane, one output float4 per thread");
+        __shared__ float s_lw[MF ? CGT : 1][W];
+        static_assert(G <= 16, "one column per lane");
         const int c = lane & 15, g = lane >> 4;
         l1 += __shfl_xor(l1, 16);
         l1 += __shfl_xor(l1, 32);
         float *so = (float *)&s_ring[wave][0];
-        static_assert(G * D * 4 <= RING_U * 16, "wave state exceeds its ring region");
-        if (c < G) {
+        static_assert(CGT * D * 4 <= RING_U * 16, "wave state exceeds its ring region");
+        if ((u32)c < cg) {
 #pragma unroll
             for (int db = 0; db < D / 16; db++)
                 *(float4 *)&so[c * D + 16 * db + 4 * g] =
@@ -1171,8 +1226,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             }
         }
         __syncthreads();
-        if (tid < G * D / 4) {
-            const int h = tid / (D / 4), d = (tid % (D / 4)) * 4;
+        for (u32 t = (u32)tid; t < cg * (D / 4); t += NT) {
+            const int h = (int)(t / (D / 4)), d = (int)(t % (D / 4)) * 4;
             float mm = s_m[0][h];
 #pragma unroll
             for (int w = 1; w < W; w++) mm = fmaxf(mm, s_m[w][h]);
@@ -1331,11 +1386,11 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         if (tid == 0) s_epoch = launches + 1u;
         __syncthreads();
         const u32 epoch = s_epoch;
-        constexpr u32 COLS = G * D / 4;
+        const u32 COLS = cg * (D / 4);
         const u32 cps = (COLS + n_split - 1) / n_split;   /* columns per slice */
         const u32 c0 = split * cps, c1 = min(c0 + cps, COLS);
         const __amdgpu_buffer_rsrc_t rrec = buf_rsrc((const float4 *)p.ws_ml + pb);
-        if (tid < G) {
+        if ((u32)tid < cg) {
             const u32 pi = (u32)tid * n_split + split;
             __builtin_amdgcn_raw_buffer_store_b128(
                 u32x4v_t{__float_as_uint(s_rec[tid].x), __float_as_uint(s_rec[tid].y), epoch,
@@ -1373,7 +1428,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             if (tid == 0)
                 __hip_atomic_store(&tags[split], epoch, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-            merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
+            merge_slice<D, W>(p, pb, r, kvh, G, cg, sq, split, cps);
             return;
         }
         if (tid == 0) {
@@ -1392,7 +1447,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        merge_slice<D, G, W>(p, pb, r, kvh, sq, split, cps);
+        merge_slice<D, W>(p, pb, r, kvh, G, cg, sq, split, cps);
         /* slices whose owner has not claimed them (yet) */
         if (wave == 0) {
             u64 todo = 0;
@@ -1410,7 +1465,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         }
         __syncthreads();
         for (u64 todo = s_todo; todo; todo &= todo - 1)
-            merge_slice<D, G, W>(p, pb, r, kvh, sq, (u32)__builtin_ctzll(todo), cps);
+            merge_slice<D, W>(p, pb, r, kvh, G, cg, sq, (u32)__builtin_ctzll(todo), cps);
         return;
     }
     if (tid == 0)
@@ -1420,8 +1475,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     if (closer && tid == 0)
         __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (!closer) return;
-    /* (m, l) pairs of the partials: G * n_split <= 2048 (ring memory) */
-    split_merge_regs<D, G, NT>(p, pb, kvh, r, sq, (float2 *)&s_ring[0][0]);
+    /* (m, l) pairs of the partials: cg * n_split <= 2048 (ring memory) */
+    split_merge_regs<D, CGT, NT>(p, pb, kvh, r, G, cg, sq, (float2 *)&s_ring[0][0]);
 }
 
 /* One decode kernel instance: entry point, K (or V) bytes per wave tile and

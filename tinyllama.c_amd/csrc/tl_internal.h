@@ -63,6 +63,8 @@ struct DecParams {
                                 NULL = partials are merged by attn_merge_kernel */
     uint32_t dist;           /* 1: every split merges its own slice of the output */
     uint32_t polls;          /* most polls per bounded wait of the split merge */
+    uint32_t rows_per_wg;    /* matrix-core tile: batch rows per workgroup group (their
+                                heads side by side as the MFMA columns); 0 or 1: one */
 };
 
 /* In-launch split merge state, per workspace (u32 words, zero at start):

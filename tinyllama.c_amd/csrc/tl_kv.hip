@@ -220,7 +220,7 @@ static void tune_seed() {
     static const char *const names[TL_TUNE_COUNT] = {
         "TL_DECODE_WGS", "TL_DECODE_MIN_KEYS", "TL_DECODE_MERGE_KERNEL", "TL_PREFILL_SPLITS",
         "TL_NO_PREFILL", "TL_DECODE_SINGLE_MERGE", "TL_DECODE_MERGE_POLLS",
-        "TL_PREFILL_APPEND_POLLS", "TL_PREFILL_SEPARATE_APPEND", "TL_DECODE_MFMA"};
+        "TL_PREFILL_APPEND_POLLS", "TL_PREFILL_SEPARATE_APPEND", "TL_DECODE_MFMA", "TL_DECODE_ROWS"};
     for (int i = 0; i < TL_TUNE_COUNT; i++) {
         const char *e = getenv(names[i]);
         g_tune[i].store(e && *e ? (u32)strtoul(e, NULL, 10) : 0u, std::memory_order_relaxed);

@@ -65,7 +65,7 @@ TUNE_DECODE_WGS, TUNE_DECODE_MIN_KEYS, TUNE_DECODE_MERGE_KERNEL = 0, 1, 2
 TUNE_PREFILL_SPLITS, TUNE_NO_PREFILL, TUNE_DECODE_SINGLE_MERGE = 3, 4, 5
 TUNE_DECODE_MERGE_POLLS = 6
 TUNE_PREFILL_APPEND_POLLS, TUNE_PREFILL_SEPARATE_APPEND = 7, 8
-TUNE_DECODE_MFMA = 9
+TUNE_DECODE_MFMA, TUNE_DECODE_ROWS = 9, 10
 
 
 class tuning:
