@@ -763,6 +763,53 @@ def split_trace(path, warmup, steps):
               f"{gap:.2f} |")
 
 
+def decode_tile_sweep(P=32768, reps=50):
+    """Decode of 1-8 batch rows of one session at P keys (rows in the cache,
+    no append) over f16 and Q8_0 caches of several shapes, per tile variant:
+    the automatic choice, the vector tile, the matrix tile with one row per
+    group and with the rows folded into its columns.  Prints one JSON line
+    per shape (us per launch)."""
+    import torch
+    import tlkv
+    lib = tlkv.lib()
+    tlkv.check(lib.tl_init(0))
+    variants = (("auto", 0, 0), ("vector", 1, 0), ("matrix_1row", 2, 1), ("matrix_fold", 2, 0))
+    for q8 in (False, True):
+        for n_head, n_kv, hd in ((8, 8, 128), (32, 8, 128), (16, 4, 128), (8, 4, 256),
+                                 (16, 8, 256), (8, 8, 64), (32, 8, 64)):
+            kd, qd = n_kv * hd, n_head * hd
+            L = (tlkv.LayerQ8 if q8 else tlkv.Layer)(P + 64, n_kv, hd)
+            rows = torch.randn((4096, kd), device="cuda")
+            app = lib.tl_kv_append_q8 if q8 else lib.tl_kv_append
+            for p0 in range(0, P, 4096):
+                tlkv.check(app(L.desc, tlkv.ptr(rows), tlkv.ptr(rows), kd, None, p0, 4096, None))
+            fn = lib.tl_attn_noappend_q8 if q8 else lib.tl_attn_noappend
+            for n in (1, 2, 4, 8):
+                q = torch.randn((n, qd), device="cuda")
+                o = torch.empty((n, qd), device="cuda")
+                a = tlkv.attn_args(q, None, None, o, None, P - n, n, n_head, hd, n_kv, 0,
+                                   1.0 / hd ** 0.5)
+                res = {}
+                for name, mf, rr in variants:
+                    with tlkv.tuning(tlkv.TUNE_DECODE_MFMA, mf), \
+                            tlkv.tuning(tlkv.TUNE_DECODE_ROWS, rr):
+                        for _ in range(5):
+                            tlkv.check(fn(L.desc, a, None))
+                        torch.cuda.synchronize()
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        for _ in range(reps):
+                            fn(L.desc, a, None)
+                        e1.record()
+                        torch.cuda.synchronize()
+                        res[name] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+                print(json.dumps({"cache": "q8_0" if q8 else "f16", "n_head": n_head,
+                                  "n_kv_head": n_kv, "head_dim": hd, "rows": n, "keys": P,
+                                  "us_per_launch": res}), flush=True)
+            del L, rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -780,7 +827,13 @@ def main():
     ap.add_argument("--split-trace", metavar="CSV",
                     help="no run: split a rocprofv3 kernel-trace CSV of a run with the same "
                          "--steps/--warmup into the config-4 decode variants, print markdown")
+    ap.add_argument("--decode-tile-sweep", action="store_true",
+                    help="no run: time decode tile variants over 1-8 batch rows and several "
+                         "shapes at 32K keys, one JSON line per shape")
     args = ap.parse_args()
+    if args.decode_tile_sweep:
+        decode_tile_sweep()
+        return
     if args.split_trace:
         split_trace(args.split_trace, args.warmup, args.steps)
         return

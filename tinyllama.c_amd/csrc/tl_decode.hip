@@ -129,7 +129,19 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
      * tiles, half of each 16-key block padding) the vector tile is faster
      * (config 5, gqa 2: 13.1 vs 13.4 us per launch). */
     const u32 tile_sel = tl_tune(TL_TUNE_DECODE_MFMA);
-    const bool mf_auto = head_dim == 64 ? G >= 2 : head_dim == 128 ? G >= (q8 ? 5u : 2u) : false;
+    /* with several batch rows the matrix tile folds up to 16 / gqa of them
+     * (8 / gqa at head_dim 256) into its columns and reads K/V once for all,
+     * where the vector tile reads them once per row: folding wins at every
+     * head_dim and cache type (measured at 32K keys: MHA head_dim 128, 8
+     * rows: 26.7 vs 128.6 us; Q8_0 head_dim 128, gqa 1, 4 rows: 24.7 vs
+     * 46.2 us; head_dim 256, gqa 4, 2 rows: 28.4 vs 45.9 us), so any fold
+     * takes the matrix tile */
+    const u32 rows_in = p.rows_per_seq ? p.rows_per_seq : 1u;
+    const u32 rmax = (head_dim == 256 ? 8u : 16u) / G;
+    const bool can_fold = fold_rows && rows_in > 1 && rmax > 1 &&
+                          !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL) && tl_tune(TL_TUNE_DECODE_ROWS) != 1;
+    const bool mf_auto = can_fold ||
+                         (head_dim == 64 ? G >= 2 : head_dim == 128 ? G >= (q8 ? 5u : 2u) : false);
     const bool mf = tile_sel == 2 || (tile_sel != 1 && mf_auto);
     switch (head_dim) {
     case 64: K = pick_kernel<64>((int)G, p.rope.rdim != 0, q8, mf); break;
