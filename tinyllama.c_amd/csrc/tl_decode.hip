@@ -123,9 +123,10 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
     /* tiles on the matrix cores where measured faster (8 kv-heads, 1K and
      * 32K keys, gqa 1-8): the f16 cache at head_dim 64 and 128 from gqa 2
      * (gqa 8: 16.3 vs 38.3 us at 32K keys; gqa 1 even); the Q8_0 cache at
-     * head_dim 64 from gqa 2 and at 128 from gqa 5 (gqa 8: 26.9 vs 57.9 us;
-     * its matrix tile holds near 26 us at 32K keys whatever the gqa, while
-     * the vector tile takes 20-26 us up to gqa 4).  At head_dim 256 (8-key
+     * head_dim 64 from gqa 2 and at 128 from gqa 4 (gqa 8: 26.9 vs 57.9 us;
+     * with two ring tiles per softmax chain the matrix tile takes 24.3 vs
+     * 24.65 us at gqa 4 and 8 kv-heads, 16.4 vs 17.9 at 4 kv-heads; gqa 1
+     * stays on the vector tile: 17.7 vs 25.9 us).  At head_dim 256 (8-key
      * tiles, half of each 16-key block padding) the vector tile is faster
      * (config 5, gqa 2: 13.1 vs 13.4 us per launch). */
     const u32 tile_sel = tl_tune(TL_TUNE_DECODE_MFMA);
@@ -141,7 +142,7 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
     const bool can_fold = fold_rows && rows_in > 1 && rmax > 1 &&
                           !tl_tune(TL_TUNE_DECODE_MERGE_KERNEL) && tl_tune(TL_TUNE_DECODE_ROWS) != 1;
     const bool mf_auto = can_fold ||
-                         (head_dim == 64 ? G >= 2 : head_dim == 128 ? G >= (q8 ? 5u : 2u) : false);
+                         (head_dim == 64 ? G >= 2 : head_dim == 128 ? G >= (q8 ? 4u : 2u) : false);
     const bool mf = tile_sel == 2 || (tile_sel != 1 && mf_auto);
     switch (head_dim) {
     case 64: K = pick_kernel<64>((int)G, p.rope.rdim != 0, q8, mf); break;

@@ -167,6 +167,11 @@ struct RCfg {
  * probabilities stay <= 2^8 and most tiles skip the rescale. */
 #define TL_DEC_TAU 8.0f
 
+/* Q8_0 ring tiles per softmax chain of the matrix-core tile: the chain's
+ * tiles share one max, one rescale decision and one exponential pass, and
+ * their LDS reads and MFMAs interleave (1: a chain per tile) */
+#define TL_DEC_Q8_CHAIN 2
+
 /* With G <= LPK every head of the group has its own lane in each key
  * group, and the softmax of a tile runs once per (key pair, head) instead
  * of once per lane: lane sub handles head sub and keeps that head's running
@@ -437,37 +442,47 @@ struct MfRows {
     bool multi;     /* more than one row */
 };
 
-template <int D, int G>
-TL_DEV void mf_softmax_pv(df4_t (&s)[(RCfg<D>::TK + 15) / 16], const uint4 *tv, u32 tbase,
-                          u32 kend, const MfRows &mr, int lane, float &m, float &l,
-                          df4_t (&O)[D / 16]) {
+/* NTL tiles' score blocks at once (tile t: s[t], V tile tv[t], first key
+ * tbase[t]): one max, one rescale decision and one running sum for all of
+ * them, so several tiles cost one softmax chain. */
+template <int D, int G, int NTL>
+TL_DEV void mf_softmax_pvn(df4_t (&s)[NTL][(RCfg<D>::TK + 15) / 16], const uint4 *const (&tv)[NTL],
+                           const u32 (&tbase)[NTL], u32 kend, const MfRows &mr, int lane,
+                           float &m, float &l, df4_t (&O)[D / 16]) {
     using C = RCfg<D>;
     constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, DB = D / 16;
     constexpr float NEG_INF = -__builtin_huge_valf();
     const int g = lane >> 4, c = lane & 15;
-    /* keys past the chunk (wave-uniform: only a chunk's last tile), the
-     * copied rows of 8-key tiles, and keys outside a column's own row */
-    const bool cols = mr.multi && (tbase < mr.ulo || tbase + (u32)TK > mr.uhi);
-    if (TK < 16 || tbase + (u32)TK > kend || cols) {
-        /* the lane's visible keys [lo, hi) as one unsigned range test
-         * (key - lo < n); a select per element, no branch */
-        const u32 lo = cols ? mr.klo : 0u;
-        const u32 hi = cols ? min(mr.khi, kend) : kend;
-        const u32 n = hi > lo ? hi - lo : 0u;
 #pragma unroll
-        for (int b = 0; b < NB; b++)
+    for (int tl = 0; tl < NTL; tl++) {
+        /* keys past the chunk (wave-uniform: only a chunk's last tiles),
+         * the copied rows of 8-key tiles, and keys outside a column's own
+         * row */
+        const u32 tb = tbase[tl];
+        const bool cols = mr.multi && (tb < mr.ulo || tb + (u32)TK > mr.uhi);
+        if (TK < 16 || tb + (u32)TK > kend || cols) {
+            /* the lane's visible keys [lo, hi) as one unsigned range test
+             * (key - lo < n); a select per element, no branch */
+            const u32 lo = cols ? mr.klo : 0u;
+            const u32 hi = cols ? min(mr.khi, kend) : kend;
+            const u32 n = hi > lo ? hi - lo : 0u;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const u32 kk = (u32)(16 * b + 4 * g + i);
-                const bool live = kk < (u32)TK && tbase + kk - lo < n;
-                s[b][i] = live ? s[b][i] : NEG_INF;
-            }
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const u32 kk = (u32)(16 * b + 4 * g + i);
+                    const bool live = kk < (u32)TK && tb + kk - lo < n;
+                    s[tl][b][i] = live ? s[tl][b][i] : NEG_INF;
+                }
+        }
     }
     float mx = NEG_INF;
 #pragma unroll
-    for (int b = 0; b < NB; b++)
+    for (int tl = 0; tl < NTL; tl++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[b][i]);
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[tl][b][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     if (__builtin_amdgcn_ballot_w64(mx > m + TL_DEC_TAU)) {
@@ -480,28 +495,46 @@ TL_DEV void mf_softmax_pv(df4_t (&s)[(RCfg<D>::TK + 15) / 16], const uint4 *tv, 
         for (int db = 0; db < DB; db++) O[db] *= a;
     }
     const float mu = (m == NEG_INF) ? 0.f : m;
-    dh4_t pb[NB];
+    dh4_t pb[NTL][NB];
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        float p[4];
+    for (int tl = 0; tl < NTL; tl++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            p[i] = fast_exp2(s[b][i] - mu);
-            l += p[i];
+        for (int b = 0; b < NB; b++) {
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = fast_exp2(s[tl][b][i] - mu);
+                l += p[i];
+            }
+            pb[tl][b] = dh4_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
         }
-        pb[b] = dh4_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-    }
-    const _Float16 *vh = (const _Float16 *)tv;
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const int t = (16 * b + 4 * g + (c >> 2)) % TK;
+    for (int tl = 0; tl < NTL; tl++) {
+        const _Float16 *vh = (const _Float16 *)tv[tl];
 #pragma unroll
-        for (int db = 0; db < DB; db++) {
-            const int x = 16 * db + 4 * (c & 3);
-            const dh4_t va = ld_tr16_h4(vh + (t * CPR + ((x >> 3) ^ (t & 1))) * 8 + (x & 7));
-            O[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb[b], O[db], 0, 0, 0);
+        for (int b = 0; b < NB; b++) {
+            const int t = (16 * b + 4 * g + (c >> 2)) % TK;
+#pragma unroll
+            for (int db = 0; db < DB; db++) {
+                const int x = 16 * db + 4 * (c & 3);
+                const dh4_t va = ld_tr16_h4(vh + (t * CPR + ((x >> 3) ^ (t & 1))) * 8 + (x & 7));
+                O[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb[tl][b], O[db], 0, 0, 0);
+            }
         }
     }
+}
+
+template <int D, int G>
+TL_DEV void mf_softmax_pv(df4_t (&s)[(RCfg<D>::TK + 15) / 16], const uint4 *tv, u32 tbase,
+                          u32 kend, const MfRows &mr, int lane, float &m, float &l,
+                          df4_t (&O)[D / 16]) {
+    constexpr int NB = (RCfg<D>::TK + 15) / 16;
+    df4_t s1[1][NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) s1[0][b] = s[b];
+    const uint4 *const tv1[1] = {tv};
+    const u32 tb1[1] = {tbase};
+    mf_softmax_pvn<D, G, 1>(s1, tv1, tb1, kend, mr, lane, m, l, O);
 }
 
 template <int D, int G>
@@ -525,8 +558,9 @@ TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32
     mf_softmax_pv<D, G>(s, tv, tbase, kend, mr, lane, m, l, O);
 }
 
-/* mfma_tile over a Q8_0 tile (int8 rows as loaded: row t at byte t*D; f16
- * scales [TK][D/32] in sk / sv).  Scores: every 32-dim step of the QK MFMA
+/* mfma_tile over NTL Q8_0 tiles at once (tile t: int8 rows as loaded in
+ * stage[t], row r at byte r*D; f16 scales [TK][D/32], K at scl[t], V at
+ * scl[t] + 64).  Scores: every 32-dim step of the QK MFMA
  * is exactly one scale block, so the exact int8 values (f16) go into the
  * MFMA and each step's result is scaled by its key's block scale in f32, as
  * the vector tile does.  V: the wave reads its int8 K fragments and V rows
@@ -535,75 +569,101 @@ TL_DEV void mfma_tile(const uint4 *tk, const uint4 *tv, const dh8_t (&qb)[D / 32
  * (4 KB: the int8 K and V halves together), and the PV step reads it as
  * one.  The LDS operations of one wave run in order, so every lane's reads
  * precede the overwrite. */
-template <int D, int G>
-TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *sk, const u16 *sv, const dh8_t (&qb)[D / 32],
-                         u32 tbase, u32 kend, const MfRows &mr, int lane, float &m, float &l,
-                         df4_t (&O)[D / 16]) {
+template <int D, int G, int NTL>
+TL_DEV void mfma_tile_q8n(uint4 *const (&stage)[NTL], const u16 *const (&scl)[NTL],
+                          const dh8_t (&qb)[D / 32], const u32 (&tbase)[NTL], u32 kend,
+                          const MfRows &mr, int lane, float &m, float &l, df4_t (&O)[D / 16]) {
     using C = RCfg<D>;
     constexpr int TK = C::TK, CPR = C::CPR, NB = (TK + 15) / 16, QS = D / 32, NSB = D / 32;
     constexpr int VU = TK * CPR / 64;              /* 8-byte V units per lane */
     const int g = lane >> 4, c = lane & 15;
-    const uint8_t *k8 = (const uint8_t *)stage, *v8 = k8 + TK * D;
-    /* every LDS read of the tile first (values, then the scales the lane
+    /* every LDS read of the tiles first (values, then the scales the lane
      * needs), so the wave waits once */
-    uint2 kw[NB][QS], vw[VU];
-    u16 ksc[NB][4][QS], vsc[VU];
+    uint2 kw[NTL][NB][QS], vw[NTL][VU];
+    u16 ksc[NTL][NB][4][QS], vsc[NTL][VU];
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const int t = (16 * b + c) % TK;
+    for (int tl = 0; tl < NTL; tl++) {
+        const uint8_t *k8 = (const uint8_t *)stage[tl], *v8 = k8 + TK * D;
 #pragma unroll
-        for (int j = 0; j < QS; j++) kw[b][j] = *(const uint2 *)(k8 + t * D + 8 * (4 * j + g));
+        for (int b = 0; b < NB; b++) {
+            const int t = (16 * b + c) % TK;
+#pragma unroll
+            for (int j = 0; j < QS; j++) kw[tl][b][j] = *(const uint2 *)(k8 + t * D + 8 * (4 * j + g));
+        }
+#pragma unroll
+        for (int k = 0; k < VU; k++) {
+            const int u = lane + 64 * k;
+            vw[tl][k] = *(const uint2 *)(v8 + (u / CPR) * D + 8 * (u % CPR));
+        }
     }
 #pragma unroll
-    for (int k = 0; k < VU; k++) {
-        const int u = lane + 64 * k;
-        vw[k] = *(const uint2 *)(v8 + (u / CPR) * D + 8 * (u % CPR));
-    }
+    for (int tl = 0; tl < NTL; tl++) {
+        const u16 *sk = scl[tl], *sv = sk + 64;
 #pragma unroll
-    for (int b = 0; b < NB; b++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const u16 *row = sk + ((16 * b + 4 * g + i) % TK) * NSB;   /* NSB scales, 4-byte aligned */
+            for (int i = 0; i < 4; i++) {
+                const u16 *row = sk + ((16 * b + 4 * g + i) % TK) * NSB;   /* NSB scales, 4-byte aligned */
 #pragma unroll
-            for (int j = 0; j < QS; j += 2) {
-                const u32 w = *(const u32 *)(row + j);
-                ksc[b][i][j] = (u16)(w & 0xffffu);
-                ksc[b][i][j + 1] = (u16)(w >> 16);
+                for (int j = 0; j < QS; j += 2) {
+                    const u32 w = *(const u32 *)(row + j);
+                    ksc[tl][b][i][j] = (u16)(w & 0xffffu);
+                    ksc[tl][b][i][j + 1] = (u16)(w >> 16);
+                }
             }
+#pragma unroll
+        for (int k = 0; k < VU; k++) {
+            const int u = lane + 64 * k;
+            vsc[tl][k] = sv[(u / CPR) * NSB + (u % CPR) / 4];
+        }
+    }
+    df4_t s[NTL][NB];
+#pragma unroll
+    for (int tl = 0; tl < NTL; tl++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            df4_t acc[QS];
+#pragma unroll
+            for (int j = 0; j < QS; j++) {
+                tl_half2 h0, h1, h2, h3;
+                i8x4_to_f16(kw[tl][b][j].x, h0, h1);
+                i8x4_to_f16(kw[tl][b][j].y, h2, h3);
+                const u32x4_t kx = {__builtin_bit_cast(u32, h0), __builtin_bit_cast(u32, h1),
+                                    __builtin_bit_cast(u32, h2), __builtin_bit_cast(u32, h3)};
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dh8_t, kx), qb[j],
+                                                                df4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
+            s[tl][b] = df4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < QS; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    s[tl][b][i] = fmaf(acc[j][i], (float)__builtin_bit_cast(_Float16, ksc[tl][b][i][j]),
+                                       s[tl][b][i]);
         }
 #pragma unroll
-    for (int k = 0; k < VU; k++) {
-        const int u = lane + 64 * k;
-        vsc[k] = sv[(u / CPR) * NSB + (u % CPR) / 4];
-    }
-    df4_t s[NB];
+    for (int tl = 0; tl < NTL; tl++)
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        df4_t acc[QS];
-#pragma unroll
-        for (int j = 0; j < QS; j++) {
-            tl_half2 h0, h1, h2, h3;
-            i8x4_to_f16(kw[b][j].x, h0, h1);
-            i8x4_to_f16(kw[b][j].y, h2, h3);
-            const u32x4_t kx = {__builtin_bit_cast(u32, h0), __builtin_bit_cast(u32, h1),
-                                __builtin_bit_cast(u32, h2), __builtin_bit_cast(u32, h3)};
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dh8_t, kx), qb[j],
-                                                            df4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        for (int k = 0; k < VU; k++) {
+            const int u = lane + 64 * k, t = u / CPR, cc = u % CPR;
+            stage[tl][t * CPR + (cc ^ (t & 1))] = q8_dequant8(vw[tl][k], (u32)vsc[tl][k]);
         }
-        s[b] = df4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < QS; j++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                s[b][i] = fmaf(acc[j][i], (float)__builtin_bit_cast(_Float16, ksc[b][i][j]), s[b][i]);
-    }
-#pragma unroll
-    for (int k = 0; k < VU; k++) {
-        const int u = lane + 64 * k, t = u / CPR, cc = u % CPR;
-        stage[t * CPR + (cc ^ (t & 1))] = q8_dequant8(vw[k], (u32)vsc[k]);
-    }
     __builtin_amdgcn_wave_barrier();
-    mf_softmax_pv<D, G>(s, stage, tbase, kend, mr, lane, m, l, O);
+    const uint4 *tv[NTL];
+#pragma unroll
+    for (int tl = 0; tl < NTL; tl++) tv[tl] = stage[tl];
+    mf_softmax_pvn<D, G, NTL>(s, tv, tbase, kend, mr, lane, m, l, O);
+}
+
+/* mfma_tile over one Q8_0 tile (scales: K at scl, V at scl + 64) */
+template <int D, int G>
+TL_DEV void mfma_tile_q8(uint4 *stage, const u16 *scl, const dh8_t (&qb)[D / 32], u32 tbase,
+                         u32 kend, const MfRows &mr, int lane, float &m, float &l,
+                         df4_t (&O)[D / 16]) {
+    uint4 *const st[1] = {stage};
+    const u16 *const sc[1] = {scl};
+    const u32 tb[1] = {tbase};
+    mfma_tile_q8n<D, G, 1>(st, sc, qb, tb, kend, mr, lane, m, l, O);
 }
 
 constexpr int pow2_floor(int x) { return x >= 16 ? 16 : x >= 8 ? 8 : x >= 4 ? 4 : x >= 2 ? 2 : 1; }
@@ -1110,7 +1170,32 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         for (int db = 0; db < D / 16; db++) O1[db] = df4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (u32 j = 0; j < nj; j++) {
+    u32 j0 = 0;
+    /* Q8_0 on the matrix cores: TL_DEC_Q8_CHAIN ring tiles per softmax
+     * chain (the ring's other tiles stay in flight meanwhile); one at
+     * head_dim 256, where two tiles' registers would spill */
+    constexpr int NC = D == 256 ? 1 : TL_DEC_Q8_CHAIN;
+    if constexpr (Q8 && MF && NC > 1) {
+        static_assert(NC < S, "tiles in flight during a chain");
+        for (; j0 + NC <= nj; j0 += NC) {
+            const u32 after = nj - NC - j0;
+            wait_tiles_q8(after < (u32)(S - NC) ? after : (u32)(S - NC));
+            uint4 *st[NC];
+            const u16 *sc[NC];
+            u32 tb[NC];
+#pragma unroll
+            for (int t = 0; t < NC; t++) {
+                st[t] = &s_ring[wave][((j0 + t) % S) * STAGE_U];
+                sc[t] = (const u16 *)&s_scl[wave][((j0 + t) % S) * 64];
+                tb[t] = kbeg + (wave + W * (j0 + t)) * TK;
+            }
+            mfma_tile_q8n<D, G, NC>(st, sc, qm, tb, kend, mr, lane, m1, l1, O1);
+#pragma unroll
+            for (int t = 0; t < NC; t++)
+                if (j0 + t + S < nj) issue(j0 + t + S);
+        }
+    }
+    for (u32 j = j0; j < nj; j++) {
         const u32 after = nj - 1 - j;
         if constexpr (Q8)
             wait_tiles_q8(after < (u32)(S - 1) ? after : (u32)(S - 1));
@@ -1140,7 +1225,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         if constexpr (Q8) {
             const u16 *ss = (const u16 *)&s_scl[wave][(j % S) * 64];
             if constexpr (MF)
-                mfma_tile_q8<D, G>(&s_ring[wave][(j % S) * STAGE_U], ss, ss + 64, qm,
+                mfma_tile_q8<D, G>(&s_ring[wave][(j % S) * STAGE_U], ss, qm,
                                    kbeg + (wave + W * j) * TK, kend, mr, lane, m1, l1, O1);
             else
                 ring_tile_q8<D, G>(st, st + UNITS / 2, ss, ss + 64, qr, kbeg + (wave + W * j) * TK,
