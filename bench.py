@@ -665,7 +665,7 @@ def run_q8(torch, tlkv, lib, sh, gen, c, steps):
                    "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                    "f16_equivalent_GBs": round(f16_bytes / (us * 1e-6) / 1e9, 1),
                    "steps": n_st, "keys": P + 1,
-                   "kernel": "attn_decode_ring_kernel<128,4,false,true,false>",
+                   "kernel": "attn_decode_ring_kernel<128,4,false,true,true>",
                    "note": "tl_attn_noappend_q8 over the contiguous Q8_0 cache; GBs counts "
                            "int8 rows + f16 scales, f16_equivalent_GBs the bytes of the same "
                            "keys in the f16 cache"},

@@ -380,6 +380,23 @@ FOLD_CASES = [
 ]
 
 
+@pytest.mark.parametrize("case", [
+    # n_head, n_kv, hd, cap, pos, n, slot table
+    (32, 8, 128, 40100, 40000, 8, "perm"),    # 16 groups, 20 splits each
+    (32, 8, 128, 70000, 66000, 1, "perm"),    # slots past 65535, 33 splits per group
+    (32, 8, 128, 40100, 40000, 8, None),      # no slot table
+])
+def test_decode_long_chunks(T, case):
+    """Launches whose 2048-key chunk limit needs more workgroups than are
+    resident (a second round of workgroups), with slot values past 65535."""
+    n_head, n_kv, hd, cap, pos, n, table = case
+    rng = np.random.default_rng(cap + n)
+    slots = rng.permutation(cap).astype(np.uint32) if table else None
+    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, 0, slots, seed=pos + n)
+    assert np.abs(out - o16).max() < TOL, case
+    assert np.abs(out - o32).max() < TOL, case
+
+
 @pytest.mark.parametrize("case", FOLD_CASES)
 def test_decode_row_folding(T, case):
     """Several batch rows of a session in one matrix-core group (their heads
@@ -399,7 +416,9 @@ def test_decode_row_folding(T, case):
         assert np.abs(out - o16).max() < TOL, (case, rows)
         assert np.abs(out - o32).max() < TOL, (case, rows)
         outs.append(out)
-    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+    # different split plans: P is rounded to f16 against different running
+    # maxima (the same bound as the prefill split test)
+    assert np.abs(outs[0] - outs[1]).max() < 3e-4
 
 
 def test_decode_batch_sessions(T):

@@ -244,7 +244,9 @@ def test_attn_q8_row_folding(T, case):
                                           seed=pos + n, ring=ring)
         assert np.abs(out - ref).max() < TOL, (case, rows)
         outs.append(out)
-    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+    # different split plans: P is rounded to f16 against different running
+    # maxima (the same bound as the prefill split test)
+    assert np.abs(outs[0] - outs[1]).max() < 3e-4
 
 
 @pytest.mark.parametrize("n", [1, 4, 40])

@@ -172,7 +172,10 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
     }
     if (R > 1 && p.window) max_vis += R - 1;   /* the rows' windows start apart */
     u64 n_groups = (u64)(n_rows_total / rows) * ((rows + R - 1) / R) * p.n_kv;
-    u32 n_split = (u32)((target + n_groups - 1) / n_groups);
+    /* splits per group: as many as fill the resident workgroups, never more
+     * (a grid a few workgroups past one resident wave runs a second round
+     * for them) */
+    u32 n_split = n_groups < target ? (u32)(target / n_groups) : 1u;
     const u32 waves = (u32)K.threads / 64;
     /* fewest keys per split: a tile for every wave at head_dim 128, for half
      * of them at 64 and 256, at most 128 keys (measured: head_dim 64, P =
