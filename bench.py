@@ -810,6 +810,48 @@ def decode_tile_sweep(P=32768, reps=50):
             del L, rows
 
 
+def attn_kernel_sweep(reps=30):
+    """OP_ATTN (tl_attn: append + attention) of 16-64 rows at 1K-16K keys,
+    as planned and on the decode kernel alone (TL_TUNE_NO_PREFILL = 1): the
+    crossover between the decode and the prefill kernel.  One JSON line per
+    shape and key count (us per launch)."""
+    import torch
+    import tlkv
+    lib = tlkv.lib()
+    tlkv.check(lib.tl_init(0))
+    for P in (1024, 2048, 4096, 8192, 16384):
+        for n_head, n_kv, hd in ((32, 8, 128), (28, 4, 128), (32, 8, 64), (8, 4, 256)):
+            kd, qd = n_kv * hd, n_head * hd
+            L = tlkv.Layer(P + 128, n_kv, hd)
+            rows = torch.randn((4096, kd), device="cuda")
+            for p0 in range(0, P, 4096):
+                tlkv.check(lib.tl_kv_append(L.desc, tlkv.ptr(rows), tlkv.ptr(rows), kd, None, p0,
+                                            min(4096, P - p0), None))
+            res = {}
+            for n in (16, 24, 32, 48, 64):
+                q = torch.randn((n, qd), device="cuda")
+                k = torch.randn((n, kd), device="cuda")
+                o = torch.empty((n, qd), device="cuda")
+                a = tlkv.attn_args(q, k, k, o, None, P, n, n_head, hd, n_kv, 0, 1.0 / hd ** 0.5)
+                for name, nopf in (("planned", 0), ("decode_kernel", 1)):
+                    with tlkv.tuning(tlkv.TUNE_NO_PREFILL, nopf):
+                        for _ in range(3):
+                            tlkv.check(lib.tl_attn(L.desc, a, None))
+                        torch.cuda.synchronize()
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        for _ in range(reps):
+                            lib.tl_attn(L.desc, a, None)
+                        e1.record()
+                        torch.cuda.synchronize()
+                        res.setdefault(f"rows{n}", {})[name] = round(
+                            e0.elapsed_time(e1) * 1e3 / reps, 2)
+            print(json.dumps({"n_head": n_head, "n_kv_head": n_kv, "head_dim": hd, "keys": P,
+                              "us_per_launch": res}), flush=True)
+            del L, rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -830,7 +872,13 @@ def main():
     ap.add_argument("--decode-tile-sweep", action="store_true",
                     help="no run: time decode tile variants over 1-8 batch rows and several "
                          "shapes at 32K keys, one JSON line per shape")
+    ap.add_argument("--attn-kernel-sweep", action="store_true",
+                    help="no run: time OP_ATTN of 16-64 rows at 1K-16K keys as planned and on "
+                         "the decode kernel alone, one JSON line per shape")
     args = ap.parse_args()
+    if args.attn_kernel_sweep:
+        attn_kernel_sweep()
+        return
     if args.decode_tile_sweep:
         decode_tile_sweep()
         return

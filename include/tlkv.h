@@ -120,7 +120,8 @@ int tl_init(int device);
 #define TL_TUNE_DECODE_MIN_KEYS     1   /* fewest keys per decode split */
 #define TL_TUNE_DECODE_MERGE_KERNEL 2   /* 1: merge decode splits in a separate launch */
 #define TL_TUNE_PREFILL_SPLITS      3   /* key splits of the prefill kernel */
-#define TL_TUNE_NO_PREFILL          4   /* 1: run every batch on the decode kernel */
+#define TL_TUNE_NO_PREFILL          4   /* 1: run every batch on the decode kernel, 2: every
+                                           batch of at least 16 rows on the prefill kernel */
 #define TL_TUNE_DECODE_SINGLE_MERGE 5   /* 1: the last split of a group merges all of it */
 #define TL_TUNE_DECODE_MERGE_POLLS  6   /* n: at most n - 1 polls per wait of the split merge */
 #define TL_TUNE_PREFILL_APPEND_POLLS 7  /* n: at most n - 1 polls per wait for the fused append */

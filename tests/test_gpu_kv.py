@@ -480,16 +480,23 @@ PREFILL_CASES = [
     (8, 4, 256, 800, 600, 64, 128, True),    # config 5 local layer (window)
     (8, 4, 256, 800, 500, 200, 0, False),    # config 5 global layer
     (16, 2, 128, 300, 7, 16, 5, True),       # smallest prefill batch, tiny window
+    (32, 8, 128, 2200, 2000, 64, 0, True),   # 64 rows x 2K keys (decode kernel when planned)
+    (28, 4, 128, 700, 600, 40, 0, False),    # 40 rows, gqa 7
 ]
 
 
+@pytest.mark.parametrize("kernel", ["auto", "prefill"])
 @pytest.mark.parametrize("case", PREFILL_CASES)
-def test_prefill_vs_oracle(T, case):
+def test_prefill_vs_oracle(T, case, kernel):
+    """Batches of 16+ rows: as planned (small rows x keys run on the decode
+    kernel) and forced onto the prefill kernel."""
+    import tlkv
     n_head, n_kv, hd, cap, pos, n, window, perm = case
     rng = np.random.default_rng(sum(case))
     slots = (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
-    out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
-                                    seed=pos + 3 * n)
+    with tlkv.tuning(tlkv.TUNE_NO_PREFILL, 2 if kernel == "prefill" else 0):
+        out, o16, o32, _, _ = _run_attn(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                        seed=pos + 3 * n)
     e16 = np.abs(out - o16).max()
     e32 = np.abs(out - o32).max()
     assert e16 < TOL, f"vs f16-cache oracle {e16}"

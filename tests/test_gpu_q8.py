@@ -205,6 +205,20 @@ def test_attn_q8_vs_oracle(T, case):
     assert np.array_equal(gv, C.v) and np.array_equal(gvs, C.vs)
 
 
+@pytest.mark.parametrize("case", [c for c in Q8_CASES if c[5] >= 16])
+def test_attn_q8_prefill_kernel_forced(T, case):
+    """Batches of 16+ rows over the Q8_0 cache on the prefill kernel, also
+    where the plan takes the decode kernel (small rows x keys)."""
+    import tlkv
+    n_head, n_kv, hd, cap, pos, n, window, perm, ring = case
+    rng = np.random.default_rng(hash(case) & 0xffff)
+    slots = None if ring else (rng.permutation(cap) if perm else np.arange(cap)).astype(np.uint32)
+    with tlkv.tuning(tlkv.TUNE_NO_PREFILL, 2):
+        out, ref, _, _ = _run_attn_q8(T, n_head, n_kv, hd, cap, pos, n, window, slots,
+                                      seed=pos + n, ring=ring)
+    assert np.abs(out - ref).max() < TOL
+
+
 @pytest.mark.parametrize("tile", ["vector", "matrix"])
 @pytest.mark.parametrize("case", [c for c in Q8_CASES if c[5] < 16] +
                          [(32, 8, 128, 33800, 33791, 1, 0, False, 0)])

@@ -51,6 +51,19 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES)
 def test_attn_rope_equals_rope_then_attn(T, case):
+    _rope_case(T, case)
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[4] >= 16])
+def test_attn_rope_prefill_kernel_forced(T, case):
+    """The batches of 16+ rows on the prefill kernel, also where the plan
+    takes the decode kernel (small rows x keys)."""
+    import tlkv
+    with tlkv.tuning(tlkv.TUNE_NO_PREFILL, 2):
+        _rope_case(T, case)
+
+
+def _rope_case(T, case):
     import tlkv
     n_head, n_kv, hd, pos, n, rdim, neox, theta = case
     lib = tlkv.lib()

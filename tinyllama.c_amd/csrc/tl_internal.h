@@ -6,6 +6,8 @@
 
 #define TL_COPY_MAX_LAYERS 64
 #define TL_PREFILL_MIN_ROWS 16
+#define TL_PREFILL_MIN_WORK 262144  /* rows x visible keys up to which the decode kernel runs */
+#define TL_DEC_FOLD_MAX_ROWS 64     /* most rows of a decode-kernel batch */
 #define TL_DEC_MAX_NEW 16          /* new rows of one fused decode launch (< TL_PREFILL_MIN_ROWS) */
 
 /* One segment of an append launch: n rows of one layer of one session. */
@@ -170,5 +172,7 @@ int tl_launch_merge(const DecParams &p, uint32_t n_rows_total, uint32_t head_dim
 
 /* MFMA chunked-prefill attention (tl_prefill.hip). */
 bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a);
+/* the batch runs on the prefill kernel (else on the decode kernel) */
+bool tl_use_prefill(const LayerView &L, const tl_attn_args *a);
 int tl_launch_prefill(const LayerView &L, const tl_attn_args *a, const RopeCfg &rope,
                       hipStream_t st, bool append = false);

@@ -681,7 +681,7 @@ static int check_args(const tl_kv_layer *L, const tl_attn_args *a) {
 static int attn_core(const tl_kv_layer *L, const tl_attn_args *a, bool append,
                      const RopeCfg &rope, hipStream_t st) {
     const LayerView lv = tl_view(L);
-    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(lv, a)) {
+    if (tl_use_prefill(lv, a)) {
         bool fused = false;
         if (append) {
             AppendParams ap;

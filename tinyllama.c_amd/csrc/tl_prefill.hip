@@ -47,9 +47,25 @@ TL_PREFILL_PICKER(tl_prefill_fn, false, false)
 /* ------------------------------------------------------------------------ */
 
 bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a) {
-    if (tl_tune(TL_TUNE_NO_PREFILL)) return false;
+    if (tl_tune(TL_TUNE_NO_PREFILL) == 1) return false;
     const u32 G = a->n_head / L.n_kv_head;
     return (L.head_dim == 64 || L.head_dim == 128 || L.head_dim == 256) && G >= 1 && G <= 8;
+}
+
+/* The prefill kernel for batches of at least TL_PREFILL_MIN_ROWS rows whose
+ * rows x visible keys exceed TL_PREFILL_MIN_WORK (or of more than
+ * TL_DEC_FOLD_MAX_ROWS rows); smaller ones run on the decode kernel, whose
+ * matrix tile folds the rows into its columns.  Measured (f16, 8 or 4
+ * kv-heads, head_dim 64-256, us per launch, decode vs prefill kernel): 64
+ * rows at 1K keys 16.0 vs 25.6, at 2K 21.0 vs 27.9; 32 rows at 4K 21.4 vs
+ * 26.3; 16 rows at 8K 19.5 vs 26.2, 24 rows 27.4 vs 27.0; 32 rows at 8K
+ * 46.9 vs 28.0; 16 rows at 16K 49.3 vs 31.8. */
+bool tl_use_prefill(const LayerView &L, const tl_attn_args *a) {
+    if (a->n < TL_PREFILL_MIN_ROWS || !tl_prefill_supported(L, a)) return false;
+    if (tl_tune(TL_TUNE_NO_PREFILL) == 2) return true;
+    const u64 keys = (u64)a->pos + a->n;
+    const u64 vis = (a->window && keys > a->window) ? a->window : keys;
+    return a->n > TL_DEC_FOLD_MAX_ROWS || (u64)a->n * vis > TL_PREFILL_MIN_WORK;
 }
 
 /* query blocks (one 32-row block per wave and q-head) per workgroup: PCfg::QB */

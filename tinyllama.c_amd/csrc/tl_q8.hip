@@ -471,7 +471,7 @@ static int attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, bool append,
         rc = append_q8(L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n, rope, st);
         if (rc) return rc;
     }
-    if (a->n >= TL_PREFILL_MIN_ROWS && tl_prefill_supported(lv, a))
+    if (tl_use_prefill(lv, a))
         return tl_launch_prefill(lv, a, rope, st);
     DecParams p;
     memset(&p, 0, sizeof(p));
