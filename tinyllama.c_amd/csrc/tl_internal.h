@@ -7,6 +7,7 @@
 #define TL_COPY_MAX_LAYERS 64
 #define TL_PREFILL_MIN_ROWS 16
 #define TL_PREFILL_MIN_WORK 262144  /* rows x visible keys up to which the decode kernel runs */
+#define TL_PREFILL_MIN_WORK_Q8 163840  /* the same over a Q8_0 cache */
 #define TL_DEC_FOLD_MAX_ROWS 64     /* most rows of a decode-kernel batch */
 #define TL_DEC_MAX_NEW 16          /* new rows of one fused decode launch (< TL_PREFILL_MIN_ROWS) */
 

@@ -59,13 +59,16 @@ bool tl_prefill_supported(const LayerView &L, const tl_attn_args *a) {
  * kv-heads, head_dim 64-256, us per launch, decode vs prefill kernel): 64
  * rows at 1K keys 16.0 vs 25.6, at 2K 21.0 vs 27.9; 32 rows at 4K 21.4 vs
  * 26.3; 16 rows at 8K 19.5 vs 26.2, 24 rows 27.4 vs 27.0; 32 rows at 8K
- * 46.9 vs 28.0; 16 rows at 16K 49.3 vs 31.8. */
+ * 46.9 vs 28.0; 16 rows at 16K 49.3 vs 31.8.  The Q8_0 cache's decode tile
+ * is dearer per key: 32 rows at 4K 27.1 vs 29.1, 48 rows 56.0 vs 32.4; 16
+ * rows at 8K 28.4 vs 30.4, 24 rows 37.5 vs 32.2. */
 bool tl_use_prefill(const LayerView &L, const tl_attn_args *a) {
     if (a->n < TL_PREFILL_MIN_ROWS || !tl_prefill_supported(L, a)) return false;
     if (tl_tune(TL_TUNE_NO_PREFILL) == 2) return true;
     const u64 keys = (u64)a->pos + a->n;
     const u64 vis = (a->window && keys > a->window) ? a->window : keys;
-    return a->n > TL_DEC_FOLD_MAX_ROWS || (u64)a->n * vis > TL_PREFILL_MIN_WORK;
+    const u64 work = L.q8 ? TL_PREFILL_MIN_WORK_Q8 : TL_PREFILL_MIN_WORK;
+    return a->n > TL_DEC_FOLD_MAX_ROWS || (u64)a->n * vis > work;
 }
 
 /* query blocks (one 32-row block per wave and q-head) per workgroup: PCfg::QB */
