@@ -763,6 +763,50 @@ def split_trace(path, warmup, steps):
               f"{gap:.2f} |")
 
 
+def split_counters(root, warmup, steps):
+    """Counter values of a profiled run (`rocprofv3 --pmc ...` CSVs under
+    `root`, any counters): the mean per dispatch of every kernel, and
+    DECODE_KERNEL's dispatches split by the order main() issues them (as
+    split_trace, then the decode_multi_row launches: 32 + min(64, steps) x 32
+    folded, the same one row per group).  Prints markdown tables."""
+    import csv
+    import glob
+    from collections import defaultdict
+    L = CFG4["L"]
+    acc = defaultdict(lambda: [0, 0.0])
+    per = defaultdict(list)
+    for path in glob.glob(os.path.join(root, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"].replace("void ", "").split("(")[0].strip()
+                key = (name, r["Counter_Name"])
+                acc[key][0] += 1
+                acc[key][1] += float(r["Counter_Value"])
+                if DECODE_KERNEL.replace(" ", "") in name.replace(" ", ""):
+                    per[r["Counter_Name"]].append((int(r["Dispatch_Id"]),
+                                                   float(r["Counter_Value"])))
+    print("| kernel | counter | dispatches | mean per dispatch |")
+    print("|---|---|---|---|")
+    for (kn, cn), (n, tot) in sorted(acc.items()):
+        print(f"| `{kn}` | {cn} | {n} | {tot / n:.1f} |")
+    n_main, n_side, n_mr = (warmup + steps) * L, min(128, steps) * L, min(64, steps) * L
+    c0 = n_main + 2 * (L + n_side)
+    phases = [("identity slot table + fused append (the timed `value` loop)", warmup * L, n_main),
+              ("contiguous cache, no append", n_main + L, n_main + L + n_side),
+              ("permuted slot table, no append", n_main + 2 * L + n_side, c0),
+              ("4 batch rows folded into one group (decode_multi_row)", c0 + L, c0 + L + n_mr),
+              ("4 batch rows, one row per group", c0 + 2 * L + n_mr, c0 + 2 * (L + n_mr))]
+    for cn, vals in sorted(per.items()):
+        vals.sort()
+        print(f"\n`{DECODE_KERNEL}`, {cn} by bench row:\n")
+        print("| row | dispatches | mean per dispatch |")
+        print("|---|---|---|")
+        for nm, a, b in phases:
+            seg = [v for _, v in vals[a:b]]
+            if seg:
+                print(f"| {nm} | {len(seg)} | {sum(seg) / len(seg):.1f} |")
+
+
 def decode_tile_sweep(P=32768, reps=50):
     """Decode of 1-8 batch rows of one session at P keys (rows in the cache,
     no append) over f16 and Q8_0 caches of several shapes, per tile variant:
@@ -869,6 +913,9 @@ def main():
     ap.add_argument("--split-trace", metavar="CSV",
                     help="no run: split a rocprofv3 kernel-trace CSV of a run with the same "
                          "--steps/--warmup into the config-4 decode variants, print markdown")
+    ap.add_argument("--split-counters", metavar="DIR",
+                    help="no run: summarise the rocprofv3 --pmc CSVs under DIR of a run with the "
+                         "same --steps/--warmup (per kernel, and the config-4 decode by bench row)")
     ap.add_argument("--decode-tile-sweep", action="store_true",
                     help="no run: time decode tile variants over 1-8 batch rows and several "
                          "shapes at 32K keys, one JSON line per shape")
@@ -884,6 +931,9 @@ def main():
         return
     if args.split_trace:
         split_trace(args.split_trace, args.warmup, args.steps)
+        return
+    if args.split_counters:
+        split_counters(args.split_counters, args.warmup, args.steps)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; runs on several GPUs "
