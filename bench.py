@@ -352,7 +352,8 @@ def run_config2(torch, tlkv, lib, sh, gen, steps=512):
 def run_config2_q8(torch, tlkv, lib, sh, gen, q, k, v, out, steps):
     """Config 2 over Q8_0 caches: the same 8 sessions x 8192 rows (quantized
     from N(0,1) rows), `steps` batched decode steps of tl_attn_decode_batch_q8
-    (one quantizing append launch + one decode launch per layer)."""
+    (one launch per layer: the decode launch quantizes and writes the new
+    rows itself)."""
     L, Hq, Hkv, d, n_seq, P0 = 28, 28, 4, 128, 8, 8192
     kd = Hkv * d
     cap = P0 + steps + 8
@@ -398,8 +399,8 @@ def run_config2_q8(torch, tlkv, lib, sh, gen, q, k, v, out, steps):
     return {"GBs": round(_gbs(nbytes, ms), 1), "steps": steps,
             "us_per_layer": round(ms * 1e3 / steps / L, 2),
             "tok_s": round(n_seq * steps / (ms / 1e3), 1),
-            "note": "Q8_0 bytes (int8 rows + f16 scales); per layer one quantizing "
-                    "append launch and one decode launch for the 8 sessions"}
+            "note": "Q8_0 bytes (int8 rows + f16 scales); per layer one decode launch for "
+                    "the 8 sessions that also quantizes and writes their new rows"}
 
 
 def run_config5(torch, tlkv, lib, sh, gen, steps=512):
@@ -578,7 +579,7 @@ def run_q8(torch, tlkv, lib, sh, gen, c, steps):
     (tl_attn_noappend_q8, MFMA kernel dequantizing its tiles), then decode
     steps over the contiguous cache at P = ctx + 1 keys: attention alone
     (tl_attn_noappend_q8, one launch) and OP_ATTN with the new row
-    (tl_attn_q8: quantizing append + attention, two launches)."""
+    (tl_attn_q8: one launch that also quantizes and writes the new row)."""
     L, Hq, Hkv, d, ub = c["L"], c["Hq"], c["Hkv"], c["d"], c["ub"]
     kd, qd = Hkv * d, Hq * d
     scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
@@ -641,7 +642,7 @@ def run_q8(torch, tlkv, lib, sh, gen, c, steps):
     us = c0.elapsed_time(c1) * 1e3 / (n_st * L)
     nbytes = decode_bytes_q8(c, P + 1)
     f16_bytes = decode_bytes(c, P + 1) - Hkv * d * 2 * 6
-    # OP_ATTN with the new row: quantizing append + attention
+    # OP_ATTN with the new row (quantized and written by the decode launch)
     a_ap = [tlkv.attn_args(q[l], k[l], v[l], out[l], None, P + 1, 1, Hq, d, Hkv, 0, scale)
             for l in range(L)]
     attn = lib.tl_attn_q8

@@ -263,6 +263,53 @@ def test_attn_q8_row_folding(T, case):
     assert np.abs(outs[0] - outs[1]).max() < 3e-4
 
 
+@pytest.mark.parametrize("case", [
+    # n_head, n_kv, hd, cap, pos, n, window, ring
+    (32, 8, 128, 4200, 4000, 1, 0, 0),        # config 4 shape
+    (16, 2, 128, 600, 200, 5, 0, 0),          # folded batch rows
+    (8, 8, 64, 1300, 1000, 15, 0, 0),         # MHA, 15 new rows
+    (8, 4, 256, 0, 3000, 3, 1024, 1026),      # ring of a windowed layer
+    (28, 4, 128, 9000, 8191, 2, 0, 0),        # gqa 7, rows across tiles
+])
+def test_attn_q8_fused_append_equals_separate(T, case):
+    """tl_attn_q8 on decode-sized batches quantizes and writes the new rows
+    inside the decode launch: the cache (values and scales) and the output
+    equal tl_kv_append_q8 followed by tl_attn_noappend_q8, bit for bit."""
+    import tlkv
+    lib = tlkv.lib()
+    n_head, n_kv, hd, cap, pos, n, window, ring = case
+    cap = ring or cap
+    rng = np.random.default_rng(pos + n)
+    kd = n_kv * hd
+    hist_k, hist_v = rows(rng, pos, kd, scale_spread=True), rows(rng, pos, kd, scale_spread=True)
+    q, k, v = rows(rng, n, n_head * hd), rows(rng, n, kd, scale_spread=True), rows(rng, n, kd)
+    slots = None if ring else rng.permutation(cap).astype(np.uint32)
+    ds = None if slots is None else dev(T, slots)
+    outs, layers = [], []
+    for fused in (True, False):
+        L = tlkv.LayerQ8(cap, n_kv, hd, ring=ring)
+        lo = max(0, pos - ring) if ring else 0
+        tlkv.check(lib.tl_kv_append_q8(L.desc, tlkv.ptr(dev(T, hist_k[lo:])),
+                                       tlkv.ptr(dev(T, hist_v[lo:])), kd, tlkv.ptr(ds), lo,
+                                       pos - lo, None))
+        out = T.zeros((n, n_head * hd), dtype=T.float32, device="cuda")
+        dk, dv = dev(T, k), dev(T, v)
+        a = tlkv.attn_args(dev(T, q), dk, dv, out, ds, pos, n, n_head, hd, n_kv, window,
+                           O.scale_of(hd))
+        if fused:
+            tlkv.check(lib.tl_attn_q8(L.desc, a, None))
+        else:
+            tlkv.check(lib.tl_kv_append_q8(L.desc, tlkv.ptr(dk), tlkv.ptr(dv), kd, tlkv.ptr(ds),
+                                           pos, n, None))
+            tlkv.check(lib.tl_attn_noappend_q8(L.desc, a, None))
+        sync(T)
+        outs.append(host(out))
+        layers.append(_q8(L))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), case
+    for x, y in zip(layers[0], layers[1]):
+        assert np.array_equal(x, y), case
+
+
 @pytest.mark.parametrize("n", [1, 4, 40])
 def test_attn_noappend_q8(T, n):
     rng = np.random.default_rng(n)

@@ -179,6 +179,30 @@ TL_DEV void i8x4_to_f16(u32 w, tl_half2 &lo, tl_half2 &hi) {
     hi = __builtin_bit_cast(tl_half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - bias;
 }
 
+/* Q8_0 quantizer (gpu.cu:1077-1086): a lane holds 8 values of a 32-value
+ * block, the block max comes from its 4-lane group (amax8, group_max<4>),
+ * d = max / 127, q = rint(x / d) with 1/d formed once; shared by the append
+ * kernel and the decode launch's fused append, so both write the same bits.
+ * 8 values of a block whose scale is 1/id -> 8 int8 in two words: */
+TL_DEV uint2 q8_pack8(const float (&x)[8], float id) {
+    u32 w[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int a = (int)rintf(x[4 * h] * id), b = (int)rintf(x[4 * h + 1] * id);
+        const int c = (int)rintf(x[4 * h + 2] * id), d = (int)rintf(x[4 * h + 3] * id);
+        w[h] = (u32)(a & 0xff) | ((u32)(b & 0xff) << 8) | ((u32)(c & 0xff) << 16) |
+               ((u32)(d & 0xff) << 24);
+    }
+    return make_uint2(w[0], w[1]);
+}
+
+TL_DEV float amax8(const float (&x)[8]) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(x[j]));
+    return m;
+}
+
 /* 8 int8 of one 32-element block and its binary16 scale d -> 8 binary16
  * values RNE(q * d) (the product is formed exactly, then rounded once) */
 TL_DEV uint4 q8_dequant8(uint2 w, u32 d_bits) {

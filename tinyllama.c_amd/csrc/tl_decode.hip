@@ -115,9 +115,10 @@ static int resident_per_cu(const void *fn, int threads) {
  * attn_merge_kernel. */
 static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u32 max_vis,
                          hipStream_t st, bool q8, bool fold_rows) {
-    if (q8) {
+    if (q8 && p.rope.rdim) {
         for (u32 i = 0; i < TL_MAX_BATCH_SEQ; i++)
-            if (p.seq[i].kin) return tl_fail(TL_EINVAL, "decode: no fused append into a Q8_0 cache");
+            if (p.seq[i].kin)
+                return tl_fail(TL_EINVAL, "decode: no fused append with RoPE into a Q8_0 cache");
     }
     DecKernel K;
     /* tiles on the matrix cores where measured faster (8 kv-heads, 1K and

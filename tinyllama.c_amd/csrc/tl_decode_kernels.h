@@ -842,6 +842,13 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     __shared__ float s_m[W][CGT];
     __shared__ uint4 s_newk[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
     __shared__ uint4 s_newv[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
+    /* Q8_0: the launch's new rows quantized as the append kernel does (int8
+     * in 8-value units, binary16 block scales); no fused append with RoPE */
+    constexpr bool Q8NEW = Q8 && !ROPE;
+    __shared__ uint2 s_nk8[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 8 : 1];
+    __shared__ uint2 s_nv8[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 8 : 1];
+    __shared__ u16 s_nks[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 32 : 1];
+    __shared__ u16 s_nvs[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 32 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -883,7 +890,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const u32 start = (p.window && n_keys0 > p.window) ? n_keys0 - p.window : 0;
     const u32 kbeg = start + split * p.chunk;
     const u32 kend = min(kbeg + p.chunk, n_keys);
-    const bool fused = !Q8 && sq.kin != nullptr;
+    const bool fused = (!Q8 || Q8NEW) && sq.kin != nullptr;
     const bool writer = fused && split == 0 && r == 0;
     const bool need_new = fused && (writer || kend > sq.pos);
     const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
@@ -964,6 +971,32 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         }
     };
 
+    /* Q8_0 fused append: a landed tile holding rows of this launch (key >=
+     * pos) gets them, and their block scales, from the staged new rows */
+    auto patch_q8 = [&](u32 j) __attribute__((always_inline)) {
+        if constexpr (Q8NEW) {
+            const u32 tb = kbeg + (wave + W * j) * TK;
+            if (!patch || tb + TK <= sq.pos) return;
+            uint2 *k8 = (uint2 *)&s_ring[wave][(j % S) * STAGE_U];   /* row t at t * D/8 */
+            uint2 *v8 = k8 + TK * (D / 8);
+#pragma unroll
+            for (int jj = 0; jj < (TK * (D / 8) + 63) / 64; jj++) {
+                const u32 u = (u32)(jj * 64 + lane);
+                const u32 key = min(tb + u / (D / 8), klast);
+                if (u < (u32)(TK * (D / 8)) && key >= sq.pos) {
+                    k8[u] = s_nk8[key - sq.pos][u % (D / 8)];
+                    v8[u] = s_nv8[key - sq.pos][u % (D / 8)];
+                }
+            }
+            u16 *ss = (u16 *)&s_scl[wave][(j % S) * 64];              /* [TK][D/32], V at +64 */
+            const u32 key = min(tb + (u32)lane / (D / 32), klast);
+            if ((u32)lane < (u32)(TK * (D / 32)) && key >= sq.pos) {
+                ss[lane] = s_nks[key - sq.pos][lane % (D / 32)];
+                ss[64 + lane] = s_nvs[key - sq.pos][lane % (D / 32)];
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    };
     const u32 npre = nj < (u32)S ? nj : (u32)S;
     /* the chunk's slots to LDS (one barrier), then the first tiles' loads */
     auto stage_and_issue = [&]() __attribute__((always_inline)) {
@@ -1118,8 +1151,23 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             s_q[tid] = make_uint4(pack_f16x2_fast(qa.x * sc, qa.y * sc), pack_f16x2_fast(qa.z * sc, qa.w * sc),
                                   pack_f16x2_fast(qc.x * sc, qc.y * sc), pack_f16x2_fast(qc.z * sc, qc.w * sc));
         if (has_new) {
-            s_newk[nrow][nc8] = cvt8_f16_regs(ka, kc);
-            s_newv[nrow][nc8] = cvt8_f16_regs(va, vc);
+            if constexpr (Q8) {
+                /* the 4 lanes of a 32-value block are an aligned group (rows
+                 * x D/8 items, D/8 a multiple of 4), all of them here */
+                const float kx[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
+                const float vx[8] = {va.x, va.y, va.z, va.w, vc.x, vc.y, vc.z, vc.w};
+                const float dk = group_max<4>(amax8(kx)) / 127.0f;
+                const float dv = group_max<4>(amax8(vx)) / 127.0f;
+                s_nk8[nrow][nc8] = q8_pack8(kx, dk > 0.0f ? 1.0f / dk : 0.0f);
+                s_nv8[nrow][nc8] = q8_pack8(vx, dv > 0.0f ? 1.0f / dv : 0.0f);
+                if ((nc8 & 3) == 0) {
+                    s_nks[nrow][nc8 / 4] = (u16)f32_to_f16_bits(dk);
+                    s_nvs[nrow][nc8 / 4] = (u16)f32_to_f16_bits(dv);
+                }
+            } else {
+                s_newk[nrow][nc8] = cvt8_f16_regs(ka, kc);
+                s_newv[nrow][nc8] = cvt8_f16_regs(va, vc);
+            }
         }
     }
     if constexpr (!ROPE) stage_and_issue();
@@ -1180,6 +1228,8 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
         for (; j0 + NC <= nj; j0 += NC) {
             const u32 after = nj - NC - j0;
             wait_tiles_q8(after < (u32)(S - NC) ? after : (u32)(S - NC));
+#pragma unroll
+            for (int t = 0; t < NC; t++) patch_q8(j0 + t);
             uint4 *st[NC];
             const u16 *sc[NC];
             u32 tb[NC];
@@ -1197,10 +1247,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     }
     for (u32 j = j0; j < nj; j++) {
         const u32 after = nj - 1 - j;
-        if constexpr (Q8)
+        if constexpr (Q8) {
             wait_tiles_q8(after < (u32)(S - 1) ? after : (u32)(S - 1));
-        else
+            patch_q8(j);
+        } else {
             wait_tiles(after < (u32)(S - 1) ? after : (u32)(S - 1));
+        }
         const uint4 *st = &s_ring[wave][(j % S) * STAGE_U];
         if constexpr (!Q8) {
             const u32 tb = kbeg + (wave + W * j) * TK;
@@ -1237,6 +1289,25 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
             ring_tile<D, G>(st, st + UNITS, qr, kbeg + (wave + W * j) * TK, kend, lane, m, l, acc);
         }
         if (j + S < nj) issue(j + S);
+    }
+    if constexpr (Q8NEW) {
+        if (writer) {
+            /* the new rows and their scales into the cache (the append
+             * kernel's layout: int8 [n_kv][cap][D], f16 [n_kv][cap][D/32]) */
+            for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {
+                const u32 row = i / VPR, c8 = i % VPR;
+                const u32 key = sq.pos + row;
+                const u32 ph = sq.ring ? key % sq.ring : (sq.slots ? sq.slots[key] : key);
+                if (ph >= sq.cap) continue;
+                const u64 prow = (u64)kvh * sq.cap + ph;
+                *(uint2 *)((uint8_t *)sq.k + prow * D + c8 * 8) = s_nk8[row][c8];
+                *(uint2 *)((uint8_t *)sq.v + prow * D + c8 * 8) = s_nv8[row][c8];
+                if ((c8 & 3) == 0) {
+                    ((u16 *)sq.ks)[prow * (D / 32) + c8 / 4] = s_nks[row][c8 / 4];
+                    ((u16 *)sq.vs)[prow * (D / 32) + c8 / 4] = s_nvs[row][c8 / 4];
+                }
+            }
+        }
     }
     if (!Q8 && writer) {
         for (u32 i = tid; i < p.rows_per_seq * VPR; i += NT) {

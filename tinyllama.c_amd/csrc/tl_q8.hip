@@ -123,26 +123,6 @@ struct Q8AppendParamsN {
 };
 typedef Q8AppendParamsN<TL_MAX_BATCH_SEQ> Q8AppendParams;
 
-/* 8 values of a block whose scale is 1/id -> 8 int8 in two words */
-TL_DEV uint2 q8_pack8(const float (&x)[8], float id) {
-    u32 w[2];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int a = (int)rintf(x[4 * h] * id), b = (int)rintf(x[4 * h + 1] * id);
-        const int c = (int)rintf(x[4 * h + 2] * id), d = (int)rintf(x[4 * h + 3] * id);
-        w[h] = (u32)(a & 0xff) | ((u32)(b & 0xff) << 8) | ((u32)(c & 0xff) << 16) |
-               ((u32)(d & 0xff) << 24);
-    }
-    return make_uint2(w[0], w[1]);
-}
-
-TL_DEV float amax8(const float (&x)[8]) {
-    float m = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(x[j]));
-    return m;
-}
-
 /* grid: (blocks, segments).  One lane per 8 elements (K RoPE'd first when
  * ROPE, by the routine rope_kernel uses, so the bits equal tl_rope then the
  * plain append); the 4 lanes of a block are an aligned group of a wave
@@ -467,14 +447,26 @@ static int attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, bool append,
     rc = tl_rope_cfg(L->head_dim, rp, rope);
     if (rc) return rc;
     if (a->n == 0) return TL_OK;
-    if (append) {
+    const bool prefill = tl_use_prefill(lv, a);
+    /* decode-sized batches without RoPE: the decode launch quantizes and
+     * writes the new rows itself */
+    const bool fuse = append && !prefill && a->n <= TL_DEC_MAX_NEW && rope.rdim == 0;
+    if (append && !fuse) {
         rc = append_q8(L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n, rope, st);
         if (rc) return rc;
     }
-    if (tl_use_prefill(lv, a))
+    if (prefill)
         return tl_launch_prefill(lv, a, rope, st);
     DecParams p;
     memset(&p, 0, sizeof(p));
+    if (fuse) {
+        Q8AppendSeg chk;
+        rc = fill_seg_q8(chk, L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n);
+        if (rc) return rc;
+        p.seq[0].kin = a->k;
+        p.seq[0].vin = a->v;
+        p.seq[0].kv_stride = a->kv_stride;
+    }
     p.seq[0].k = (const u16 *)L->k;
     p.seq[0].v = (const u16 *)L->v;
     p.seq[0].ks = (const u16 *)L->ks;
@@ -549,12 +541,13 @@ extern "C" int tl_attn_decode_batch_q8(const tl_decode_seq_q8 *seqs, uint32_t n_
         p.seq[i].cap = s->layer.cap;
         p.seq[i].ring = s->layer.ring;
         p.seq[i].pos = s->pos;
+        p.seq[i].kin = s->k;                /* appended by the decode launch */
+        p.seq[i].vin = s->v;
+        p.seq[i].kv_stride = a.kv_stride;
         const u32 nk = s->pos + 1;
         const u32 vis = (window && nk > window) ? window : nk;
         if (vis > max_vis) max_vis = vis;
     }
-    int rc = launch_append_q8(ap, n_seq, (hipStream_t)stream);
-    if (rc) return rc;
     p.rows_per_seq = 1;
     p.n_kv = L0->n_kv_head;
     p.n_head = n_head;
