@@ -387,7 +387,8 @@ def test_decode_batch_q8_sessions(T, window):
 
 
 @pytest.mark.parametrize("neox,rdim,n,window", [(0, 128, 1, 0), (1, 128, 3, 0), (1, 64, 40, 0),
-                                                 (0, 128, 24, 100), (1, 128, 1, 200)])
+                                                 (0, 128, 24, 100), (1, 128, 1, 200),
+                                                 (1, 128, 4, 0), (0, 64, 9, 0)])
 def test_attn_rope_q8_equals_rope_then_attn(T, neox, rdim, n, window):
     """tl_attn_rope_q8 (K rotated before quantizing, q while staged) gives the
     same bits as tl_rope on q and k followed by tl_attn_q8: outputs, values

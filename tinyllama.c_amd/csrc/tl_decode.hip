@@ -115,10 +115,11 @@ static int resident_per_cu(const void *fn, int threads) {
  * attn_merge_kernel. */
 static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u32 max_vis,
                          hipStream_t st, bool q8, bool fold_rows) {
-    if (q8 && p.rope.rdim) {
+    if (q8 && p.rope.rdim && p.rows_per_seq > TL_DEC_Q8_ROPE_NEW) {
         for (u32 i = 0; i < TL_MAX_BATCH_SEQ; i++)
             if (p.seq[i].kin)
-                return tl_fail(TL_EINVAL, "decode: no fused append with RoPE into a Q8_0 cache");
+                return tl_fail(TL_EINVAL, "decode: fused append with RoPE into a Q8_0 cache: "
+                                          "at most %d rows", TL_DEC_Q8_ROPE_NEW);
     }
     DecKernel K;
     /* tiles on the matrix cores where measured faster (8 kv-heads, 1K and

@@ -843,8 +843,9 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     __shared__ uint4 s_newk[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
     __shared__ uint4 s_newv[Q8 ? 1 : TL_DEC_MAX_NEW][D / 8];
     /* Q8_0: the launch's new rows quantized as the append kernel does (int8
-     * in 8-value units, binary16 block scales); no fused append with RoPE */
-    constexpr bool Q8NEW = Q8 && !ROPE;
+     * in 8-value units, binary16 block scales).  With RoPE the rotated K rows
+     * pass through s_nv8 as f32 first (at most TL_DEC_Q8_ROPE_NEW rows) */
+    constexpr bool Q8NEW = Q8;
     __shared__ uint2 s_nk8[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 8 : 1];
     __shared__ uint2 s_nv8[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 8 : 1];
     __shared__ u16 s_nks[Q8NEW ? TL_DEC_MAX_NEW : 1][Q8NEW ? D / 32 : 1];
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     const u32 start = (p.window && n_keys0 > p.window) ? n_keys0 - p.window : 0;
     const u32 kbeg = start + split * p.chunk;
     const u32 kend = min(kbeg + p.chunk, n_keys);
-    const bool fused = (!Q8 || Q8NEW) && sq.kin != nullptr;
+    const bool fused = sq.kin != nullptr && (!(Q8 && ROPE) || p.rows_per_seq <= TL_DEC_Q8_ROPE_NEW);
     const bool writer = fused && split == 0 && r == 0;
     const bool need_new = fused && (writer || kend > sq.pos);
     const float *qb = sq.q + (u64)r * p.q_stride + (u64)kvh * G * D;
@@ -1114,17 +1115,53 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
                     rope_cs(i, p.rope.rdim, p.rope.theta, sq.pos + row, c, sn);
                     rope_rot(kx[j], ky[j], c, sn, x, y);
                 }
-                u16 *k16 = (u16 *)s_newk[row];
-                k16[ia] = (u16)f32_to_f16_bits(x);
-                k16[ib] = (u16)f32_to_f16_bits(y);
+                if constexpr (Q8) {
+                    float *kf = (float *)&s_nv8[0][0] + row * D;   /* f32 rows, quantized below */
+                    kf[ia] = x;
+                    kf[ib] = y;
+                } else {
+                    u16 *k16 = (u16 *)s_newk[row];
+                    k16[ia] = (u16)f32_to_f16_bits(x);
+                    k16[ib] = (u16)f32_to_f16_bits(y);
+                }
             }
         }
+        if constexpr (!Q8) {
 #pragma unroll
-        for (int j = 0; j < VI; j++) {
-            const u32 i = tid + j * NT;
-            if (i < nvu) s_newv[i / VPR][i % VPR] = cvt8_f16_regs(va[j], vc[j]);
+            for (int j = 0; j < VI; j++) {
+                const u32 i = tid + j * NT;
+                if (i < nvu) s_newv[i / VPR][i % VPR] = cvt8_f16_regs(va[j], vc[j]);
+            }
         }
         __syncthreads();   /* q and the new rows */
+        if constexpr (Q8) {
+            /* the rotated K rows (f32 over s_nv8) and the V rows (registers:
+             * item tid, VI == 1) to Q8_0, one 8-value unit per thread; the
+             * 4 lanes of a block are an aligned group */
+            static_assert(VI == 1 && TL_DEC_Q8_ROPE_NEW * D * 4 <= (int)sizeof(s_nv8), "staging");
+            const bool has_new = (u32)tid < nvu;
+            const u32 nrow = (u32)tid / VPR, nc8 = (u32)tid % VPR;
+            float kq[8];
+            if (has_new) {
+                const float *kf = (const float *)&s_nv8[0][0] + nrow * D + nc8 * 8;
+#pragma unroll
+                for (int e = 0; e < 8; e++) kq[e] = kf[e];
+            }
+            __syncthreads();   /* every f32 read before the int8 rows overwrite them */
+            if (has_new) {
+                const float vq[8] = {va[0].x, va[0].y, va[0].z, va[0].w,
+                                     vc[0].x, vc[0].y, vc[0].z, vc[0].w};
+                const float dk = group_max<4>(amax8(kq)) / 127.0f;
+                const float dv = group_max<4>(amax8(vq)) / 127.0f;
+                s_nk8[nrow][nc8] = q8_pack8(kq, dk > 0.0f ? 1.0f / dk : 0.0f);
+                s_nv8[nrow][nc8] = q8_pack8(vq, dv > 0.0f ? 1.0f / dv : 0.0f);
+                if ((nc8 & 3) == 0) {
+                    s_nks[nrow][nc8 / 4] = (u16)f32_to_f16_bits(dk);
+                    s_nvs[nrow][nc8 / 4] = (u16)f32_to_f16_bits(dv);
+                }
+            }
+            __syncthreads();   /* the quantized rows */
+        }
     } else {
         /* one q item and at most one new-row item per thread (G * D / 8 and
          * TL_DEC_MAX_NEW * D / 8 are at most NT): all loads first */

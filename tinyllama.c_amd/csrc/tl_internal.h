@@ -10,6 +10,7 @@
 #define TL_PREFILL_MIN_WORK_Q8 163840  /* the same over a Q8_0 cache */
 #define TL_DEC_FOLD_MAX_ROWS 64     /* most rows of a decode-kernel batch */
 #define TL_DEC_MAX_NEW 16          /* new rows of one fused decode launch (< TL_PREFILL_MIN_ROWS) */
+#define TL_DEC_Q8_ROPE_NEW 4       /* ... into a Q8_0 cache with RoPE (f32 staging of rotated K) */
 
 /* One segment of an append launch: n rows of one layer of one session. */
 /* RoPE applied on the fly (rdim == 0: none).  Same math as rope_kernel. */

@@ -448,9 +448,10 @@ static int attn_q8(const tl_kv_layer_q8 *L, const tl_attn_args *a, bool append,
     if (rc) return rc;
     if (a->n == 0) return TL_OK;
     const bool prefill = tl_use_prefill(lv, a);
-    /* decode-sized batches without RoPE: the decode launch quantizes and
-     * writes the new rows itself */
-    const bool fuse = append && !prefill && a->n <= TL_DEC_MAX_NEW && rope.rdim == 0;
+    /* decode-sized batches (with RoPE: up to TL_DEC_Q8_ROPE_NEW rows): the
+     * decode launch quantizes and writes the new rows itself */
+    const bool fuse = append && !prefill && a->n <= TL_DEC_MAX_NEW &&
+                      (rope.rdim == 0 || a->n <= TL_DEC_Q8_ROPE_NEW);
     if (append && !fuse) {
         rc = append_q8(L, a->k, a->v, a->kv_stride, a->slots, a->pos, a->n, rope, st);
         if (rc) return rc;
