@@ -190,7 +190,18 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
     const u32 max_split = (max_vis + min_keys - 1) / min_keys;
     const u32 min_split = (max_vis + TL_DEC_MAX_CHUNK - 1) / TL_DEC_MAX_CHUNK;
     if (n_split > max_split) n_split = max_split;
-    if (n_split < min_split) n_split = min_split;
+    if (n_split < min_split) {
+        /* the chunk limit needs more workgroups than one resident round:
+         * fill whole rounds evenly instead of leaving a partial last round
+         * of full-length chunks */
+        n_split = min_split;
+        const u64 wgs = (u64)n_split * n_groups;
+        if (wgs > target) {
+            const u64 rounds = (wgs + target - 1) / target;
+            const u64 even = rounds * target / n_groups;
+            if (even > n_split) n_split = (u32)(even < max_split ? even : max_split);
+        }
+    }
     if (n_split < 1) n_split = 1;
     const u32 chunk = (max_vis + n_split - 1) / n_split;
     n_split = (max_vis + chunk - 1) / chunk;
