@@ -808,6 +808,44 @@ def split_counters(root, warmup, steps):
                 print(f"| {nm} | {len(seg)} | {sum(seg) / len(seg):.1f} |")
 
 
+def long_context_sweep(reps=50):
+    """Single-row decode (tl_attn_noappend, identity slot table) of the
+    Llama-3-8B shape at 66K-131K keys, past the point where the 2048-key
+    chunk limit needs more than one round of workgroups.  One JSON line per
+    key count (us per launch, GB/s of K/V bytes)."""
+    import torch
+    import tlkv
+    lib = tlkv.lib()
+    tlkv.check(lib.tl_init(0))
+    n_head, n_kv, hd = CFG4["Hq"], CFG4["Hkv"], CFG4["d"]
+    kd, qd = n_kv * hd, n_head * hd
+    for P in (66000, 80000, 100000, 131000):
+        cap = P + 64
+        L = tlkv.Layer(cap, n_kv, hd)
+        rows = torch.randn((4096, kd), device="cuda")
+        for p0 in range(0, P, 4096):
+            tlkv.check(lib.tl_kv_append(L.desc, tlkv.ptr(rows), tlkv.ptr(rows), kd, None, p0,
+                                        min(4096, P - p0), None))
+        slots = torch.arange(cap, dtype=torch.int32, device="cuda")
+        q = torch.randn((1, qd), device="cuda")
+        o = torch.empty((1, qd), device="cuda")
+        a = tlkv.attn_args(q, None, None, o, slots, P - 1, 1, n_head, hd, n_kv, 0, 1 / hd ** 0.5)
+        for _ in range(5):
+            tlkv.check(lib.tl_attn_noappend(L.desc, a, None))
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            lib.tl_attn_noappend(L.desc, a, None)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        print(json.dumps({"keys": P, "us_per_launch": round(us, 2),
+                          "GBs": round(P * kd * 4 / (us * 1e-6) / 1e9, 1)}), flush=True)
+        del L, rows, slots
+
+
 def decode_tile_sweep(P=32768, reps=50):
     """Decode of 1-8 batch rows of one session at P keys (rows in the cache,
     no append) over f16 and Q8_0 caches of several shapes, per tile variant:
@@ -920,10 +958,15 @@ def main():
     ap.add_argument("--decode-tile-sweep", action="store_true",
                     help="no run: time decode tile variants over 1-8 batch rows and several "
                          "shapes at 32K keys, one JSON line per shape")
+    ap.add_argument("--long-context-sweep", action="store_true",
+                    help="no run: single-row decode at 66K-131K keys, one JSON line per key count")
     ap.add_argument("--attn-kernel-sweep", action="store_true",
                     help="no run: time OP_ATTN of 16-64 rows at 1K-16K keys as planned and on "
                          "the decode kernel alone, one JSON line per shape")
     args = ap.parse_args()
+    if args.long_context_sweep:
+        long_context_sweep()
+        return
     if args.attn_kernel_sweep:
         attn_kernel_sweep()
         return
