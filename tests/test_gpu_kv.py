@@ -382,13 +382,14 @@ FOLD_CASES = [
 
 @pytest.mark.parametrize("case", [
     # n_head, n_kv, hd, cap, pos, n, slot table
-    (32, 8, 128, 40100, 40000, 8, "perm"),    # 16 groups, 20 splits each
-    (32, 8, 128, 70000, 66000, 1, "perm"),    # slots past 65535, 33 splits per group
-    (32, 8, 128, 40100, 40000, 8, None),      # no slot table
+    (32, 8, 128, 40100, 40000, 8, "perm"),    # 16 groups x 16 splits of 2501 keys: u16 slots
+    (32, 8, 128, 70000, 66000, 1, "perm"),    # slots past 65535: u32, 33+ splits in even rounds
+    (32, 8, 128, 40100, 40000, 8, None),      # no slot table: no chunk limit
 ])
 def test_decode_long_chunks(T, case):
-    """Launches whose 2048-key chunk limit needs more workgroups than are
-    resident (a second round of workgroups), with slot values past 65535."""
+    """Chunks past 2048 keys per workgroup: the u16-slot instance for pools of
+    at most 65536 rows, u32 slots (every value kept) and whole even rounds of
+    workgroups above that, and no limit without a slot table."""
     n_head, n_kv, hd, cap, pos, n, table = case
     rng = np.random.default_rng(cap + n)
     slots = rng.permutation(cap).astype(np.uint32) if table else None

@@ -188,7 +188,18 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
     const u32 min_tiles = head_dim == 128 ? waves : waves / 2;
     const u32 min_keys = tuned(TL_TUNE_DECODE_MIN_KEYS, min_tiles * tk < 128 ? min_tiles * tk : 128);
     const u32 max_split = (max_vis + min_keys - 1) / min_keys;
-    const u32 min_split = (max_vis + TL_DEC_MAX_CHUNK - 1) / TL_DEC_MAX_CHUNK;
+    /* keys per workgroup: limited by the slot-table staging only (u32
+     * indices, or u16 ones in the matrix-core f16 instances when every
+     * staged pool has at most 65536 rows); launches without a slot table
+     * stage nothing */
+    bool any_staged = false, s16_ok = mf && !q8;
+    for (u32 i = 0; i < n_rows_total / rows && i < TL_MAX_BATCH_SEQ; i++)
+        if (p.seq[i].slots && !p.seq[i].ring) {
+            any_staged = true;
+            if (p.seq[i].cap > 65536u) s16_ok = false;
+        }
+    const u32 max_chunk = !any_staged ? 0xffffffffu : s16_ok ? TL_DEC_MAX_CHUNK16 : TL_DEC_MAX_CHUNK;
+    const u32 min_split = (u32)(((u64)max_vis + max_chunk - 1) / max_chunk);
     if (n_split > max_split) n_split = max_split;
     if (n_split < min_split) {
         /* the chunk limit needs more workgroups than one resident round:
@@ -209,6 +220,12 @@ static int launch_decode(DecParams &p, u32 n_rows_total, u32 head_dim, u32 G, u3
         return tl_fail(TL_EINVAL, "decode: %u keys need %u splits", max_vis, n_split);
     p.chunk = chunk;
     p.n_split = n_split;
+    if (any_staged && chunk > TL_DEC_MAX_CHUNK) {
+        /* measured: the u16 staging chosen at run time cost every launch
+         * 0.4 us, so it is an instance of its own */
+        K = tl_pick_decode_s16((int)head_dim, (int)G, p.rope.rdim != 0);
+        if (!K.fn) return tl_fail(TL_EINVAL, "decode: no u16-slot instance for gqa %u", G);
+    }
     p.counters = nullptr;
     p.dist = 0;
     const bool in_kernel_merge = n_split > 1 && R * G * n_split <= 2048 &&

@@ -816,8 +816,8 @@ TL_DEV void merge_slice(const DecParams &p, u32 pb, u32 r, u32 kvh, u32 gh, u32 
  * the rows staged from the f32 input. */
 #define TL_RING_WAVES 8
 #define TL_RING_STAGES 2
-template <int D, int G, bool ROPE, bool Q8, bool MF>
-__global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
+template <int D, int G, bool ROPE, bool Q8, bool MF, bool S16>
+__device__ __attribute__((always_inline)) inline void decode_ring_body(const DecParams &p) {
     using C = RCfg<D>;
     constexpr int LPK = C::LPK, CPR = C::CPR, TK = C::TK, UNITS = C::UNITS, LD = C::LD;
     /* a Q8_0 tile is half the bytes of an f16 one: twice the stages in the
@@ -898,10 +898,12 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     /* physical rows of the chunk's keys */
     const bool staged = (sq.ring == 0) && (sq.slots != nullptr);
+    /* S16: the slots staged as u16, twice as many in the same LDS */
+    u16 *const s_slot16 = (u16 *)&s_slot[0];
     /* the chunk's slots are loaded here and stored to LDS after q and the new
      * rows have been requested too, so the prologue waits for one round
      * trip, not one per load */
-    constexpr int SPT = TL_DEC_MAX_CHUNK / NT;      /* slots per thread */
+    constexpr int SPT = (S16 ? TL_DEC_MAX_CHUNK16 : TL_DEC_MAX_CHUNK) / NT;   /* slots per thread */
     u32 slot_v[SPT];
     if (staged) {
 #pragma unroll
@@ -931,7 +933,9 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 
     auto phys = [&](u32 key) -> u32 {
         if (sq.ring) return key % sq.ring;
-        return staged ? s_slot[key - kbeg] : key;
+        if (!staged) return key;
+        if constexpr (S16) return (u32)s_slot16[key - kbeg];
+        return s_slot[key - kbeg];
     };
     /* unit u = jj*64 + lane of a K (or V) tile holds chunk (u % CPR) ^ (row & 1)
      * of tile row u / CPR.  Rows past the chunk load its last row (their
@@ -1005,7 +1009,13 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
 #pragma unroll
             for (int j = 0; j < SPT; j++) {
                 const u32 i = tid + j * NT;
-                if (kbeg + i < kend) s_slot[i] = slot_v[j] < sq.cap ? slot_v[j] : 0u;
+                if (kbeg + i < kend) {
+                    const u32 ph = slot_v[j] < sq.cap ? slot_v[j] : 0u;
+                    if constexpr (S16)
+                        s_slot16[i] = (u16)ph;
+                    else
+                        s_slot[i] = ph;
+                }
             }
         }
         __syncthreads();
@@ -1672,6 +1682,21 @@ __global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(co
     split_merge_regs<D, CGT, NT>(p, pb, kvh, r, G, cg, sq, (float2 *)&s_ring[0][0]);
 }
 
+/* The kernel: slot indices staged as u32, at most TL_DEC_MAX_CHUNK keys per
+ * workgroup when a slot table is staged. */
+template <int D, int G, bool ROPE, bool Q8, bool MF>
+__global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel(const DecParams p) {
+    decode_ring_body<D, G, ROPE, Q8, MF, false>(p);
+}
+
+/* The same with slot indices staged as u16 (pools of at most 65536 rows), up
+ * to TL_DEC_MAX_CHUNK16 keys per workgroup: launches whose chunks exceed
+ * TL_DEC_MAX_CHUNK (f16 cache, matrix-core tile; tl_decode_s16.hip). */
+template <int D, int G, bool ROPE, bool MF>
+__global__ __launch_bounds__(64 * TL_RING_WAVES) void attn_decode_ring_kernel_s16(const DecParams p) {
+    decode_ring_body<D, G, ROPE, false, MF, true>(p);
+}
+
 /* One decode kernel instance: entry point, K (or V) bytes per wave tile and
  * threads per workgroup.  The RoPE-fusing instances are separate so the
  * plain ones carry none of its code. */
@@ -1683,4 +1708,6 @@ struct DecKernel {
 
 /* the Q8_0 instances (tl_decode_q8.hip) */
 DecKernel tl_pick_decode_q8(int D, int G, bool rope, bool mf);
+/* the u16-slot instances (f16 cache, matrix-core tile; tl_decode_s16.hip) */
+DecKernel tl_pick_decode_s16(int D, int G, bool rope);
 

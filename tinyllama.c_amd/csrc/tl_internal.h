@@ -152,6 +152,7 @@ uint32_t tl_tune(int key);
 
 /* Most keys one decode workgroup handles (its slot indices are staged in LDS). */
 #define TL_DEC_MAX_CHUNK 2048
+#define TL_DEC_MAX_CHUNK16 4096   /* ... staged as u16 (pools of at most 65536 rows) */
 /* split partials for a launch on `st`: the stream's own workspace (grown on
  * demand), or inside a TlWsFixed scope the fixed region (TL_ERANGE when it
  * is too small; nothing is allocated) */
