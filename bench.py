@@ -829,20 +829,23 @@ def long_context_sweep(reps=50):
         slots = torch.arange(cap, dtype=torch.int32, device="cuda")
         q = torch.randn((1, qd), device="cuda")
         o = torch.empty((1, qd), device="cuda")
-        a = tlkv.attn_args(q, None, None, o, slots, P - 1, 1, n_head, hd, n_kv, 0, 1 / hd ** 0.5)
-        for _ in range(5):
-            tlkv.check(lib.tl_attn_noappend(L.desc, a, None))
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            lib.tl_attn_noappend(L.desc, a, None)
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
-        print(json.dumps({"keys": P, "us_per_launch": round(us, 2),
-                          "GBs": round(P * kd * 4 / (us * 1e-6) / 1e9, 1)}), flush=True)
+        res = {}
+        for name, sl in (("slot_table", slots), ("contiguous", None)):
+            a = tlkv.attn_args(q, None, None, o, sl, P - 1, 1, n_head, hd, n_kv, 0, 1 / hd ** 0.5)
+            for _ in range(5):
+                tlkv.check(lib.tl_attn_noappend(L.desc, a, None))
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                lib.tl_attn_noappend(L.desc, a, None)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            res[name] = {"us_per_launch": round(us, 2),
+                         "GBs": round(P * kd * 4 / (us * 1e-6) / 1e9, 1)}
+        print(json.dumps({"keys": P, **res}), flush=True)
         del L, rows, slots
 
 
